@@ -49,6 +49,33 @@ static inline uint64_t tkey64(double d) {
 static inline float rmaxf(float a, float b) { return isnan(a) ? b : (isnan(b) ? a : (a > b ? a : b)); }
 static inline double rmax(double a, double b) { return isnan(a) ? b : (isnan(b) ? a : (a > b ? a : b)); }
 
+/* Sum of v[0..V) in the device's reduction order (see tco_params.dev_*). */
+static float dev_order_sum(const float* v, size_t V, size_t row, const tco_params* p) {
+  int items = p->dev_items, threads = p->dev_threads;
+  long long shift = (long long)(((long long)row * p->dev_ld) % p->dev_align);
+  int waves = threads / 64;
+  float total = 0.0f;
+  for (int w = 0; w < waves; w++) {
+    float lane[64];
+    for (int l = 0; l < 64; l++) {
+      long long t = (long long)w * 64 + l;
+      float part = 0.0f;
+      for (int i = 0; i < items; i++) {
+        long long e = t * items + i - shift;
+        if (e >= 0 && e < (long long)V) part += v[e];
+      }
+      lane[l] = part;
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+      float nxt[64];
+      for (int l = 0; l < 64; l++) nxt[l] = lane[l] + lane[l ^ o];
+      memcpy(lane, nxt, sizeof lane);
+    }
+    total = (w == 0) ? lane[0] : total + lane[0];
+  }
+  return total;
+}
+
 static int cmp_u64(const void* a, const void* b) {
   uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
   return (x > y) - (x < y);
@@ -595,12 +622,20 @@ static int row_qwen(const tco_params* p, float* x, size_t V, const uint32_t* ids
 }
 
 /* cosyvoice3: llm.rs:517-538 */
-static int row_cosy(const tco_params* p, float* x, size_t V, const uint32_t* hist, size_t n_hist,
-                    float u0, float u1, uint32_t* tok, uint32_t* flags, row_verify* rv) {
+static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const uint32_t* hist,
+                    size_t n_hist, float u0, float u1, uint32_t* tok, uint32_t* flags, row_verify* rv) {
   if (p->eos_id >= 0) {
     for (size_t i = 0; i < V; i++) x[i] = x[i] + ((size_t)p->eos_id == i ? -INFINITY : 0.0f);
   }
-  tco_softmax_last_dim(x, V);
+  if (p->dev_threads > 0) {
+    float max = -INFINITY;
+    for (size_t i = 0; i < V; i++) max = rmaxf(max, x[i]);
+    for (size_t i = 0; i < V; i++) x[i] = expf(x[i] - max);
+    float sum = dev_order_sum(x, V, row, p);
+    for (size_t i = 0; i < V; i++) x[i] /= sum;
+  } else {
+    tco_softmax_last_dim(x, V);
+  }
   int used = 0;
   uint32_t nc = 0;
   uint32_t* cids = (uint32_t*)malloc((p->top_k + 1) * sizeof(uint32_t) + 4);
@@ -639,10 +674,23 @@ static int row_cosy(const tco_params* p, float* x, size_t V, const uint32_t* his
 
 /* indextts: generation.rs:643-666 for one row with beam score 0, then
  * sample_without_replacement with n = 1 (generation.rs:280-303). */
-static int row_indextts(const tco_params* p, float* x, size_t V, const uint32_t* ids, size_t n_ids,
-                        double u, uint32_t* tok, uint32_t* flags, row_verify* rv) {
+static int row_indextts(const tco_params* p, float* x, size_t V, size_t row, const uint32_t* ids,
+                        size_t n_ids, double u, uint32_t* tok, uint32_t* flags, row_verify* rv) {
   (void)flags;
-  tco_idx_log_softmax(x, V);
+  if (p->dev_threads > 0) {
+    float max = -INFINITY;
+    for (size_t i = 0; i < V; i++) max = rmaxf(max, x[i]);
+    if (isfinite(max)) {
+      float* e = (float*)malloc(V * sizeof(float));
+      for (size_t i = 0; i < V; i++) e[i] = (float)exp((double)(x[i] - max)); /* correctly rounded */
+      float sum = dev_order_sum(e, V, row, p);
+      float log_sum = (float)log((double)sum);
+      for (size_t i = 0; i < V; i++) x[i] = (x[i] - max) - log_sum;
+      free(e);
+    }
+  } else {
+    tco_idx_log_softmax(x, V);
+  }
   if (p->penalty != 1.0) tco_idx_penalty(x, V, ids, n_ids, p->penalty);
   if (p->typical) tco_idx_typical(x, V, p->typical_mass, 2);
   if (p->temperature != 1.0) tco_idx_temperature(x, V, p->temperature);
@@ -697,13 +745,13 @@ static int row_moss(const tco_params* p, float* x, size_t V, const uint32_t* his
   qsort(ranked, V, sizeof(uint64_t), cmp_u64);
   if (temp == 0.0f) {
     *tok = (uint32_t)ranked[0];
-    if (V > 1 && x[(uint32_t)ranked[0]] == x[(uint32_t)ranked[1]]) *flags |= TCO_FLAG_TIE_CUT;
+    if (V > 1 && ranked[0] >> 32 == ranked[1] >> 32) *flags |= TCO_FLAG_TIE_CUT;
     free(ranked);
     return TCO_OK;
   }
   size_t k = p->top_k < V ? p->top_k : V;
   if (k == 0) { free(ranked); return TCO_EINVAL; } /* ranked[0] would panic */
-  if (k < V && x[(uint32_t)ranked[k - 1]] == x[(uint32_t)ranked[k]]) *flags |= TCO_FLAG_TIE_CUT;
+  if (k < V && ranked[k - 1] >> 32 == ranked[k] >> 32) *flags |= TCO_FLAG_TIE_CUT;
   float maximum = x[(uint32_t)ranked[0]];
   double* w = (double*)malloc(k * sizeof(double));
   for (size_t i = 0; i < k; i++) w[i] = (double)expf((x[(uint32_t)ranked[i]] - maximum) / temp);
@@ -715,7 +763,7 @@ static int row_moss(const tco_params* p, float* x, size_t V, const uint32_t* his
     cumulative += w[i] / total;
     if (cumulative > p->top_p) { keep = i + 1; break; }
   }
-  if (keep < k && x[(uint32_t)ranked[keep - 1]] == x[(uint32_t)ranked[keep]]) *flags |= TCO_FLAG_TIE_CUT;
+  if (keep < k && ranked[keep - 1] >> 32 == ranked[keep] >> 32) *flags |= TCO_FLAG_TIE_CUT;
   double s = -0.0;
   for (size_t i = 0; i < keep; i++) s += w[i];
   double draw = u * s;
@@ -847,10 +895,12 @@ static void sample_one_row(const tco_params* p, const float* logits, size_t r, s
   switch (p->variant) {
     case TCO_QWEN: st = row_qwen(p, x, V, ids, n_ids, ((const float*)uniforms)[r], &tok, &flags, rv); break;
     case TCO_COSY_RAS:
-      st = row_cosy(p, x, V, ids, n_ids, ((const float*)uniforms)[2 * r], ((const float*)uniforms)[2 * r + 1],
-                    &tok, &flags, rv);
+      st = row_cosy(p, x, V, r, ids, n_ids, ((const float*)uniforms)[2 * r],
+                    ((const float*)uniforms)[2 * r + 1], &tok, &flags, rv);
       break;
-    case TCO_INDEXTTS: st = row_indextts(p, x, V, ids, n_ids, ((const double*)uniforms)[r], &tok, &flags, rv); break;
+    case TCO_INDEXTTS:
+      st = row_indextts(p, x, V, r, ids, n_ids, ((const double*)uniforms)[r], &tok, &flags, rv);
+      break;
     case TCO_MOSS: st = row_moss(p, x, V, ids, n_ids, ((const double*)uniforms)[r], &tok, &flags, rv); break;
     case TCO_MOSS_NANO: st = row_nano(p, x, V, ids, n_ids, ((const double*)uniforms)[r], &tok, &flags, rv); break;
     default: st = TCO_EINVAL;

@@ -1,0 +1,89 @@
+"""Build recipe for libtalechime_hip.so (gfx950) and its generated tables.
+
+    python -m talechime_amd.build
+
+Steps:
+  1. compile and run csrc/gen_expf_table.c (host, gcc) to produce
+     csrc/_gen/expf_glibc_exc.inc -- skipped when the include is newer than the
+     generator and tc_math.h;
+  2. hipcc --offload-arch=gfx950 -shared the kernels and the C ABI into
+     talechime_amd/libtalechime_hip.so.
+
+Floating-point flags are part of the contract: no contraction (the kernels
+reproduce unfused reference arithmetic; explicit fma() stays fused), denormals
+preserved, IEEE-correct f32 division and square root, and no packed-FP32
+instructions.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(PKG, "csrc")
+GEN = os.path.join(CSRC, "_gen")
+ROOT = os.path.dirname(PKG)
+LIB = os.path.join(PKG, "libtalechime_hip.so")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def _newer(target: str, *deps: str) -> bool:
+    if not os.path.exists(target):
+        return False
+    t = os.path.getmtime(target)
+    return all(os.path.getmtime(d) <= t for d in deps)
+
+
+def gen_tables(force: bool = False) -> None:
+    os.makedirs(GEN, exist_ok=True)
+    inc = os.path.join(GEN, "expf_glibc_exc.inc")
+    src = os.path.join(CSRC, "gen_expf_table.c")
+    hdr = os.path.join(CSRC, "tc_math.h")
+    if not force and _newer(inc, src, hdr):
+        return
+    exe = os.path.join(GEN, "gen_expf_table")
+    subprocess.run(["gcc", "-O2", "-fopenmp", "-fno-fast-math", "-ffp-contract=off", "-o", exe, src, "-lm"],
+                   check=True)
+    tmp = inc + ".tmp"
+    subprocess.run([exe, tmp], check=True)
+    os.replace(tmp, inc)
+
+
+def hipcc() -> str:
+    for c in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if c and os.path.exists(c):
+            return c
+    raise RuntimeError("hipcc not found")
+
+
+def build_lib() -> str:
+    srcs = [os.path.join(CSRC, "sampler.hip")]
+    out_tmp = LIB + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *srcs, "-o", out_tmp]
+    subprocess.run(cmd, check=True)
+    os.replace(out_tmp, LIB)
+    return LIB
+
+
+def build(force_tables: bool = False) -> str:
+    gen_tables(force_tables)
+    return build_lib()
+
+
+if __name__ == "__main__":
+    print(build(force_tables="--force" in sys.argv))

@@ -1,0 +1,1317 @@
+// sampler.hip -- per-step token sampler kernels for gfx950 and the C ABI
+// declared in include/talechime_hip.h.
+//
+// One workgroup samples one row.  The row is streamed from HBM once with
+// 16-byte loads and stays in registers (ITEMS consecutive elements per
+// thread); the history ids become a byte map in LDS; the top-k threshold is a
+// four-pass radix select over 32-bit order keys with LDS histograms; the
+// survivors are compacted into LDS in vocabulary order with a block scan; the
+// order-dependent steps (the reference's sequential f32/f64 sums, cumulative
+// cut-offs and inverse-CDF walks) run over the survivors in exactly the
+// reference's order.
+//
+// Variants and the reference code each kernel follows (talechime repository):
+//   k_qwen      crates/qwen3-tts/src/generation/sampling.rs:169-219, 224-328, 334-395,
+//               tts.rs:44-51, synthesis.rs:1228-1279
+//   k_indextts  crates/indextts/src/generation.rs:95-194, 280-303, 643-676
+//   k_cosy      crates/cosyvoice3/src/llm.rs:517-604
+//   k_moss      crates/moss-tts/src/sampling.rs:22-85
+//   k_nano      crates/moss-tts/src/nano/sampling.rs:11-75
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <string>
+
+#include "../../include/talechime_hip.h"
+#include "tc_device.h"
+
+namespace tc {
+
+constexpr int kSurvCap = 1024;      // survivors held in LDS per row
+constexpr int kMaxVocabReg = 16384; // register-resident rows: V + alignment <= 1024 * 16
+
+struct RowArgs {
+  const void* logits;
+  long long ld;
+  int V;
+  int rows;
+  const uint32_t* hist_off;
+  const uint32_t* hist_ids;
+  int hist_mode;
+  const float* pen_mask;
+  const float* add_mask;
+  const void* uniforms;
+  uint32_t* out_ids;
+  int32_t* out_status;
+  uint32_t* out_flags;
+  uint32_t cap;
+  uint32_t* topk_count;
+  uint32_t* topk_ids;
+  uint32_t* keep_count;
+  uint32_t* keep_ids;
+  float* keep_probs;
+  // parameters, prepared on the host
+  int do_pen;
+  float pen_f;    // penalty as f32
+  float inv_pen;  // qwen: 1.0f / pen_f
+  int do_temp;    // qwen: affine temperature on; others: divide by t_f
+  float tmul;     // qwen: (f32)(1 / T)
+  float t_f;      // (f32)T
+  int greedy;     // qwen: T < 0.01
+  int K;          // top-k selection size (0 = none)
+  int top_k;      // raw top_k
+  int do_topp;
+  float top_p_f;
+  double top_p_d;
+  int min_keep;
+  int eos_id;
+  int exclude_id;
+  int ras_win;
+  float ras_thresh;  // (f32)win * tau
+};
+
+struct SurvLds {
+  uint64_t key[kSurvCap];
+  double w[kSurvCap];
+  float val[kSurvCap];
+  float e[kSurvCap];
+  uint32_t idx[kSurvCap];
+  uint8_t flag[kSurvCap];
+};
+
+// ---------------------------------------------------------------- shared steps
+
+__device__ __forceinline__ void hist_range(const RowArgs& a, int row, uint32_t* h0, uint32_t* h1) {
+  if (a.hist_ids == nullptr || a.hist_off == nullptr) {
+    *h0 = *h1 = 0;
+  } else if (a.hist_mode == TC_HIST_BROADCAST) {
+    *h0 = a.hist_off[0];
+    *h1 = a.hist_off[1];
+  } else {
+    *h0 = a.hist_off[row];
+    *h1 = a.hist_off[row + 1];
+  }
+}
+
+// Byte map of the ids in the row's history (ids >= V ignored).  Returns true if
+// some id was >= V.
+__device__ bool build_seen(const RowArgs& a, int row, uint8_t* seen, BlockScratch& s) {
+  const int V = a.V;
+  uint32_t* w = reinterpret_cast<uint32_t*>(seen);
+  for (int i = threadIdx.x; i < (V + 3) / 4; i += blockDim.x) w[i] = 0u;
+  __syncthreads();
+  uint32_t h0, h1;
+  hist_range(a, row, &h0, &h1);
+  uint32_t oob = 0;
+  for (uint32_t j = h0 + threadIdx.x; j < h1; j += blockDim.x) {
+    uint32_t id = a.hist_ids[j];
+    if (id < (uint32_t)V) seen[id] = 1;
+    else oob = 1;
+  }
+  __syncthreads();
+  return block_or_u(oob, s) != 0u;
+}
+
+// Ordered compaction of the selected elements into LDS (vocabulary order).
+// Returns the number selected (may exceed kSurvCap; then only the count is valid).
+template <int ITEMS>
+__device__ uint32_t compact(const float (&x)[ITEMS], uint32_t sel, int e0, SurvLds& sv, BlockScratch& s) {
+  uint32_t c = __builtin_popcount(sel);
+  uint32_t total;
+  uint32_t pos = block_excl_scan(c, s, &total);
+  if (total <= (uint32_t)kSurvCap) {
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((sel >> i) & 1u) {
+        sv.val[pos] = x[i];
+        sv.idx[pos] = (uint32_t)(e0 + i);
+        ++pos;
+      }
+  }
+  __syncthreads();
+  return total;
+}
+
+__device__ void write_topk(const RowArgs& a, int row, const SurvLds& sv, uint32_t n) {
+  if (a.topk_count == nullptr) return;
+  if (threadIdx.x == 0) a.topk_count[row] = n;
+  if (n > (uint32_t)kSurvCap) return;  // only the count is known
+  uint32_t m = n < a.cap ? n : a.cap;
+  for (uint32_t j = threadIdx.x; j < m; j += blockDim.x) a.topk_ids[(size_t)row * a.cap + j] = sv.idx[j];
+}
+
+// Rank-order sort of the n survivors: keys built by the caller in sv.key[0..n),
+// padded to a power of two.
+__device__ void sort_survivors(SurvLds& sv, uint32_t n) {
+  int n_pad = next_pow2((int)n < 2 ? 2 : (int)n);
+  for (int j = (int)n + threadIdx.x; j < n_pad; j += blockDim.x) sv.key[j] = ~0ull;
+  __syncthreads();
+  block_bitonic_sort(sv.key, n_pad);
+}
+
+__device__ __forceinline__ void finish_row(const RowArgs& a, int row, uint32_t tok, int32_t st, uint32_t flags) {
+  if (threadIdx.x == 0) {
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = flags;
+  }
+}
+
+__device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
+  if (threadIdx.x == 0) {
+    if (a.topk_count) a.topk_count[row] = 0;
+    if (a.keep_count) a.keep_count[row] = 0;
+  }
+}
+
+// ================================================================ qwen
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_qwen(RowArgs a) {
+  __shared__ uint8_t s_seen[kMaxVocabReg];
+  __shared__ SurvLds sv;
+  __shared__ uint32_t s_hist[256];
+  __shared__ BlockScratch s;
+  __shared__ uint32_t s_out[4];
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  const bool use_seen = a.do_pen && a.hist_mode != TC_HIST_MASK;
+  if (use_seen) build_seen(a, row, s_seen, s);
+
+  // caller chain (synthesis.rs:1238-1276) then temperature (sampling.rs:175-184)
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    const int e = e0 + i;
+    float v = x[i];
+    if (a.do_pen) {
+      bool pen = use_seen ? (s_seen[e] != 0) : (a.pen_mask[e] > 0.0f);
+      if (pen) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
+    }
+    if (a.add_mask) v = v + a.add_mask[e];
+    if (e == a.eos_id) v = -__builtin_inff();
+    if (a.do_temp) v = v * a.tmul + 0.0f;
+    x[i] = v;
+  }
+
+  if (a.greedy) {
+    // candle argmax: first index whose value is strictly greater (NaN skipped)
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if (!((vm >> i) & 1u) || __builtin_isnan(x[i])) continue;
+      uint64_t k = ((uint64_t)ckey(x[i]) << 32) | (uint64_t)(~(uint32_t)(e0 + i));
+      best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      uint64_t other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    uint64_t* wb = sv.key;
+    if (lane_id() == 0) wb[wave_id()] = best;
+    if (t == 0) s_out[0] = 0u;
+    __syncthreads();
+    // x[0] NaN: the reference never updates its accumulator and returns 0
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (e0 + i == 0 && __builtin_isnan(x[i])) s_out[0] = 1u;
+    __syncthreads();
+    if (t == 0) {
+      uint64_t b = 0;
+      for (int w = 0; w < num_waves(); ++w) b = wb[w] > b ? wb[w] : b;
+      uint32_t tok = (b == 0 || s_out[0]) ? 0u : ~(uint32_t)(b & 0xffffffffu);
+      a.out_ids[row] = tok;
+      if (a.out_status) a.out_status[row] = TC_OK;
+      if (a.out_flags) a.out_flags[row] = TC_FLAG_GREEDY;
+    }
+    no_verify(a, row);
+    return;
+  }
+
+  // top-k (sampling.rs:224-249): keep v >= k-th largest, ties kept
+  uint32_t key[ITEMS];
+  uint32_t sel = 0, nanm = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    key[i] = 0u;
+    if (!((vm >> i) & 1u)) continue;
+    if (__builtin_isnan(x[i])) { nanm |= 1u << i; continue; }
+    key[i] = ckey(x[i]);
+    sel |= 1u << i;
+  }
+  uint32_t flags = block_or_u(nanm, s) ? (uint32_t)TC_FLAG_NAN_ROW : 0u;
+  float thr = -__builtin_inff();
+  if (a.K > 0) {
+    uint32_t kk;
+    if (block_kth_largest<ITEMS>(key, sel, (uint32_t)a.K, s_hist, s, &kk)) thr = untkey(kk);
+  }
+  uint32_t surv = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((sel >> i) & 1u) && x[i] >= thr && x[i] != -__builtin_inff()) surv |= 1u << i;
+  const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
+  write_topk(a, row, sv, n);
+  if (n > (uint32_t)kSurvCap) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, flags);
+    if (t == 0 && a.keep_count) a.keep_count[row] = 0;
+    return;
+  }
+  if (n == 0) {  // every entry -inf (or NaN): the reference's CDF is NaN -> index 0
+    finish_row(a, row, 0u, TC_OK, flags);
+    if (t == 0 && a.keep_count) a.keep_count[row] = 0;
+    return;
+  }
+  // softmax numerators over the survivors; the row max is the largest survivor
+  float m = -__builtin_inff();
+  for (uint32_t j = t; j < n; j += blockDim.x) m = rmaxf(m, sv.val[j]);
+  const float vmax = block_max(m, s);
+  for (uint32_t j = t; j < n; j += blockDim.x) {
+    sv.e[j] = expf_glibc(sv.val[j] - vmax);
+    sv.flag[j] = a.do_topp ? 0 : 1;
+    if (a.do_topp) sv.key[j] = ((uint64_t)(~ckey(sv.val[j])) << 32) | (uint64_t)j;
+  }
+  __syncthreads();
+  if (a.do_topp) {
+    // top-p (sampling.rs:255-299): rank order = value descending, id ascending
+    sort_survivors(sv, n);
+    if (t == 0) {
+      float S = -0.0f;
+      for (uint32_t r = 0; r < n; ++r) S += sv.e[(uint32_t)sv.key[r]];
+      float cum = 0.0f;
+      uint32_t cut = n;
+      for (uint32_t r = 0; r < n; ++r) {
+        cum += sv.e[(uint32_t)sv.key[r]] / S;
+        if (cum > a.top_p_f) { cut = r + 1; break; }
+      }
+      if (cut < n && sv.val[(uint32_t)sv.key[cut - 1]] == sv.val[(uint32_t)sv.key[cut]])
+        flags |= TC_FLAG_TIE_CUT;
+      for (uint32_t r = 0; r < cut; ++r) sv.flag[(uint32_t)sv.key[r]] = 1;
+      s_out[1] = flags;
+    }
+    __syncthreads();
+    flags = s_out[1];
+  }
+  // softmax + multinomial in vocabulary order (sampling.rs:302-328)
+  if (t == 0) {
+    float S2 = 0.0f;
+    for (uint32_t j = 0; j < n; ++j)
+      if (sv.flag[j]) S2 += sv.e[j];
+    const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+    uint32_t tok = 0;
+    if (u > 0.0f) {
+      float cum = 0.0f;
+      for (uint32_t j = 0; j < n; ++j) {
+        if (!sv.flag[j]) continue;
+        cum += sv.e[j] / S2;
+        if (cum >= u) { tok = sv.idx[j]; break; }
+      }
+    }
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = TC_OK;
+    if (a.out_flags) a.out_flags[row] = flags;
+    s_out[2] = __float_as_uint(S2);
+  }
+  if (a.keep_count) {
+    __syncthreads();
+    const float S2 = __uint_as_float(s_out[2]);
+    if (t == 0) {
+      uint32_t c = 0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.flag[j]) {
+          if (c < a.cap) {
+            a.keep_ids[(size_t)row * a.cap + c] = sv.idx[j];
+            a.keep_probs[(size_t)row * a.cap + c] = sv.e[j] / S2;
+          }
+          ++c;
+        }
+      a.keep_count[row] = c;
+    }
+  }
+}
+
+// ================================================================ indextts
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_indextts(RowArgs a) {
+  __shared__ uint8_t s_seen[kMaxVocabReg];
+  __shared__ SurvLds sv;
+  __shared__ uint32_t s_hist[256];
+  __shared__ BlockScratch s;
+  __shared__ uint32_t s_out[4];
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  if (a.do_pen) build_seen(a, row, s_seen, s);
+
+  // log_softmax (generation.rs:95-105)
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((vm >> i) & 1u) m = rmaxf(m, x[i]);
+  const float mx = block_max(m, s);
+  if (__builtin_isfinite(mx)) {
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((vm >> i) & 1u) part += tc_expf_cr(x[i] - mx);
+    const float S = block_sum(part, s);
+    const float L = tc_logf_cr(S);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) x[i] = (x[i] - mx) - L;
+  }
+  // repetition penalty on the log-probs (generation.rs:122-134), temperature (137-142)
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    float v = x[i];
+    if (a.do_pen && s_seen[e0 + i]) v = v < 0.0f ? v * a.pen_f : v / a.pen_f;
+    if (a.do_temp) v = v / a.t_f;
+    x[i] = v;
+  }
+  // top-k (generation.rs:148-161): drop scores strictly below the k-th largest (total order)
+  float kth = -__builtin_inff();
+  bool cut = false;
+  if (a.K > 0 && a.K < V) {
+    uint32_t key[ITEMS];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
+    uint32_t kk;
+    if (block_kth_largest<ITEMS>(key, vm, (uint32_t)a.K, s_hist, s, &kk)) {
+      kth = untkey(kk);
+      cut = true;
+    }
+  }
+  uint32_t surv = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && !(cut && x[i] < kth) && x[i] != -__builtin_inff()) surv |= 1u << i;
+  const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
+  if (n > (uint32_t)kSurvCap) {
+    write_topk(a, row, sv, n);
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    if (t == 0 && a.keep_count) a.keep_count[row] = 0;
+    return;
+  }
+  // verification set: finite-or-not survivors of top-k, excluding -inf
+  write_topk(a, row, sv, n);
+  for (uint32_t j = t; j < n; j += blockDim.x) sv.flag[j] = 1;  // 1 = still present
+  __syncthreads();
+  if (a.do_topp && n > 0) {
+    // top-p (generation.rs:169-194): f64 softmax over the row (dropped entries are
+    // exactly zero), ascending stable order by total_cmp, remove cum <= 1 - p,
+    // keep the min_keep largest.
+    double md = -__builtin_inf();
+    for (uint32_t j = t; j < n; j += blockDim.x) md = rmaxd(md, (double)sv.val[j]);
+    const double mxd = block_max_d(md, s);
+    const bool fin = __builtin_isfinite(mxd);
+    for (uint32_t j = t; j < n; j += blockDim.x) {
+      sv.w[j] = fin ? tc_exp_d((double)sv.val[j] - mxd) : 0.0;
+      sv.key[j] = ((uint64_t)tkey(sv.val[j]) << 32) | (uint64_t)j;
+    }
+    __syncthreads();
+    sort_survivors(sv, n);
+    if (t == 0) {
+      double sum = -0.0;
+      if (fin)
+        for (uint32_t j = 0; j < n; ++j) sum += sv.w[j];
+      double cum = 0.0;
+      const double lim = 1.0 - a.top_p_d;
+      for (uint32_t r = 0; r < n; ++r) {
+        const uint32_t j = (uint32_t)sv.key[r];
+        const double p = fin ? sv.w[j] / sum : 0.0;
+        cum += p;
+        if (cum <= lim) sv.flag[j] = 0;
+      }
+      for (uint32_t r = 0; r < n && r < (uint32_t)a.min_keep; ++r) sv.flag[(uint32_t)sv.key[n - 1 - r]] = 1;
+    }
+    __syncthreads();
+  }
+  // sample_without_replacement, one draw (generation.rs:280-303), vocab order over live
+  if (t == 0) {
+    uint32_t nl = 0;
+    double mxl = -__builtin_inf();
+    for (uint32_t j = 0; j < n; ++j) {
+      if (sv.flag[j] && __builtin_isfinite(sv.val[j])) {
+        sv.flag[j] = 2;
+        ++nl;
+        mxl = rmaxd(mxl, (double)sv.val[j] + 0.0);
+      }
+    }
+    uint32_t tok = 0;
+    int32_t st = TC_OK;
+    if (nl < 1) {
+      st = TC_ETOOFEW;
+    } else {
+      double sum = -0.0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.flag[j] == 2) { sv.w[j] = tc_exp_d(((double)sv.val[j] + 0.0) - mxl); sum += sv.w[j]; }
+      double total = -0.0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.flag[j] == 2) { sv.w[j] = sv.w[j] / sum; total += sv.w[j]; }
+      const double uu = reinterpret_cast<const double*>(a.uniforms)[row] * total;
+      double acc = 0.0;
+      uint32_t last = 0xffffffffu, pick = 0xffffffffu;
+      for (uint32_t j = 0; j < n; ++j) {
+        if (sv.flag[j] != 2) continue;
+        if (last == 0xffffffffu) last = j;  // last_positive starts at live[0]
+        const double w = sv.w[j];
+        if (w <= 0.0) continue;
+        last = j;
+        acc += w;
+        if (acc > uu) { pick = j; break; }
+      }
+      tok = sv.idx[pick != 0xffffffffu ? pick : last];
+    }
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = 0u;
+    s_out[0] = nl;
+  }
+  if (a.keep_count) {
+    __syncthreads();
+    if (t == 0) {
+      uint32_t c = 0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.flag[j] == 2) {
+          if (c < a.cap) {
+            a.keep_ids[(size_t)row * a.cap + c] = sv.idx[j];
+            a.keep_probs[(size_t)row * a.cap + c] = (float)sv.w[j];
+          }
+          ++c;
+        }
+      a.keep_count[row] = c;
+    }
+  }
+}
+
+// ================================================================ cosyvoice3
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_cosy(RowArgs a) {
+  __shared__ uint8_t s_seen[kMaxVocabReg];  // staging for the fallback CDF
+  __shared__ SurvLds sv;
+  __shared__ uint32_t s_hist[256];
+  __shared__ BlockScratch s;
+  __shared__ uint32_t s_out[4];
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  // ignore_eos mask (llm.rs:525-529), softmax (candle softmax_last_dim)
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    if (a.eos_id >= 0) x[i] = x[i] + (e0 + i == a.eos_id ? -__builtin_inff() : 0.0f);
+    m = rmaxf(m, x[i]);
+  }
+  const float mx = block_max(m, s);
+  float part = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    x[i] = expf_glibc(x[i] - mx);
+    part += x[i];
+  }
+  const float S = block_sum(part, s);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) x[i] = x[i] / S;  // probabilities
+  // nucleus (llm.rs:556-592): rank by (prob desc, id asc); at most top_k candidates
+  const uint32_t nvalid = (uint32_t)V;
+  uint32_t K = (a.top_k > 0 && (uint32_t)a.top_k < nvalid) ? (uint32_t)a.top_k : nvalid;
+  uint32_t surv = vm;
+  if (K < nvalid) {
+    uint32_t key[ITEMS];
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
+    uint32_t kk;
+    if (block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk)) {
+      surv = 0;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+        if (((vm >> i) & 1u) && key[i] >= kk) surv |= 1u << i;
+    }
+  }
+  const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
+  if (n > (uint32_t)kSurvCap) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  for (uint32_t j = t; j < n; j += blockDim.x) {
+    sv.key[j] = ((uint64_t)(~tkey(sv.val[j])) << 32) | (uint64_t)j;
+    sv.flag[j] = 0;
+  }
+  __syncthreads();
+  sort_survivors(sv, n);
+  if (t == 0) {
+    float cum = 0.0f;
+    uint32_t nc = 0;
+    for (uint32_t r = 0; r < n; ++r) {
+      if (cum < a.top_p_f && nc < (uint32_t)a.top_k) {
+        cum += sv.val[(uint32_t)sv.key[r]];
+        ++nc;
+      } else {
+        break;
+      }
+    }
+    uint32_t top;
+    if (nc == 0) {
+      top = sv.idx[(uint32_t)sv.key[0]];
+    } else {
+      float total = -0.0f;
+      for (uint32_t r = 0; r < nc; ++r) total += sv.val[(uint32_t)sv.key[r]];
+      const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row] * total;
+      float acc = 0.0f;
+      top = sv.idx[(uint32_t)sv.key[nc - 1]];
+      for (uint32_t r = 0; r < nc; ++r) {
+        acc += sv.val[(uint32_t)sv.key[r]];
+        if (pick < acc) { top = sv.idx[(uint32_t)sv.key[r]]; break; }
+      }
+    }
+    for (uint32_t r = 0; r < nc; ++r) sv.flag[(uint32_t)sv.key[r]] = 1;
+    s_out[0] = top;
+    s_out[1] = nc;
+  }
+  __syncthreads();
+  const uint32_t top = s_out[0];
+  // repetition window (llm.rs:532-536)
+  uint32_t h0, h1;
+  hist_range(a, row, &h0, &h1);
+  const uint32_t w0 = (h1 - h0) > (uint32_t)a.ras_win ? h1 - (uint32_t)a.ras_win : h0;
+  uint32_t rep = 0;
+  for (uint32_t j = w0 + t; j < h1; j += blockDim.x) rep += a.hist_ids[j] == top;
+  rep = block_sum_u(rep, s);
+  uint32_t tok = top, flags = 0;
+  if ((float)rep >= a.ras_thresh) {
+    // random_sample_probs (llm.rs:594-604): sequential CDF over the whole row
+    flags = TC_FLAG_RAS;
+    float* stage = reinterpret_cast<float*>(s_seen);
+    constexpr int kChunk = kMaxVocabReg / 4;
+    const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row + 1];
+    float acc = 0.0f;
+    uint32_t found = 0xffffffffu;
+    for (int c0 = 0; c0 < V; c0 += kChunk) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const int e = e0 + i;
+        if (((vm >> i) & 1u) && e >= c0 && e < c0 + kChunk) stage[e - c0] = x[i];
+      }
+      __syncthreads();
+      if (t == 0 && found == 0xffffffffu) {
+        const int c1 = (c0 + kChunk < V) ? c0 + kChunk : V;
+        for (int e = c0; e < c1; ++e) {
+          acc += stage[e - c0];
+          if (pick < acc) { found = (uint32_t)e; break; }
+        }
+        s_out[2] = found;
+      }
+      __syncthreads();
+      found = s_out[2];
+      if (found != 0xffffffffu) break;
+    }
+    tok = found != 0xffffffffu ? found : (uint32_t)(V - 1);
+  }
+  finish_row(a, row, tok, TC_OK, flags);
+  if (a.topk_count) {
+    const uint32_t nc = s_out[1];
+    __syncthreads();
+    if (t == 0) {
+      uint32_t c = 0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.flag[j]) {
+          if (c < a.cap) {
+            a.topk_ids[(size_t)row * a.cap + c] = sv.idx[j];
+            a.keep_ids[(size_t)row * a.cap + c] = sv.idx[j];
+            a.keep_probs[(size_t)row * a.cap + c] = sv.val[j];
+          }
+          ++c;
+        }
+      a.topk_count[row] = nc;
+      a.keep_count[row] = nc;
+    }
+  }
+}
+
+// ================================================================ moss
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_moss(RowArgs a) {
+  __shared__ uint8_t s_seen[kMaxVocabReg];
+  __shared__ SurvLds sv;
+  __shared__ uint32_t s_hist[256];
+  __shared__ BlockScratch s;
+  __shared__ uint32_t s_out[4];
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  if (a.do_pen) build_seen(a, row, s_seen, s);
+  uint32_t bad = 0, fin = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    const int e = e0 + i;
+    float v = x[i];
+    if (a.do_pen && s_seen[e]) v = v < 0.0f ? v * a.pen_f : v / a.pen_f;
+    if (e == a.exclude_id) v = -__builtin_inff();
+    x[i] = v;
+    bad |= __builtin_isnan(v) ? 1u : 0u;
+    fin |= __builtin_isfinite(v) ? 1u : 0u;
+  }
+  bad = block_or_u(bad, s);
+  fin = block_or_u(fin, s);
+  if (bad || !fin) {  // sampling.rs:51-54
+    finish_row(a, row, 0u, TC_ENONFINITE, 0u);
+    no_verify(a, row);
+    return;
+  }
+  const uint32_t K = a.greedy ? 1u : (uint32_t)(a.top_k < V ? a.top_k : V);
+  uint32_t key[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
+  uint32_t kk = 0;
+  block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk);
+  uint32_t surv = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && key[i] >= kk) surv |= 1u << i;
+  const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
+  if (n > (uint32_t)kSurvCap) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  for (uint32_t j = t; j < n; j += blockDim.x) sv.key[j] = ((uint64_t)(~tkey(sv.val[j])) << 32) | (uint64_t)j;
+  __syncthreads();
+  sort_survivors(sv, n);
+  // ranked[0..K) = the first K keys; ties beyond K mean the reference's unstable
+  // sort could have kept another id
+  uint32_t flags = n > K ? (uint32_t)TC_FLAG_TIE_CUT : 0u;
+  if (a.greedy) {  // temperature == 0: ranked[0]
+    finish_row(a, row, sv.idx[(uint32_t)sv.key[0]], TC_OK, flags);
+    no_verify(a, row);
+    return;
+  }
+  const float maximum = sv.val[(uint32_t)sv.key[0]];
+  for (uint32_t r = t; r < K; r += blockDim.x)
+    sv.w[r] = (double)expf_glibc((sv.val[(uint32_t)sv.key[r]] - maximum) / a.t_f);
+  __syncthreads();
+  if (t == 0) {
+    double total = -0.0;
+    for (uint32_t r = 0; r < K; ++r) total += sv.w[r];
+    double cum = 0.0;
+    uint32_t keep = K;
+    for (uint32_t r = 0; r < K; ++r) {
+      cum += sv.w[r] / total;
+      if (cum > a.top_p_d) { keep = r + 1; break; }
+    }
+    if (keep < K && sv.key[keep - 1] >> 32 == sv.key[keep] >> 32) flags |= TC_FLAG_TIE_CUT;
+    double sw = -0.0;
+    for (uint32_t r = 0; r < keep; ++r) sw += sv.w[r];
+    double draw = reinterpret_cast<const double*>(a.uniforms)[row] * sw;
+    uint32_t tok = sv.idx[(uint32_t)sv.key[keep - 1]];
+    for (uint32_t r = 0; r < keep; ++r) {
+      draw -= sv.w[r];
+      if (draw <= 0.0) { tok = sv.idx[(uint32_t)sv.key[r]]; break; }
+    }
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = TC_OK;
+    if (a.out_flags) a.out_flags[row] = flags;
+    s_out[0] = keep;
+    s.d[0] = sw;
+  }
+  if (a.topk_count) {
+    __syncthreads();
+    const uint32_t keep = s_out[0];
+    const double sw = s.d[0];
+    // ids in ascending order: mark ranks, then walk the vocab-ordered survivors
+    for (uint32_t r = t; r < n; r += blockDim.x) sv.flag[(uint32_t)sv.key[r]] = r < K ? (r < keep ? 2 : 1) : 0;
+    __syncthreads();
+    for (uint32_t r = t; r < K; r += blockDim.x) sv.e[(uint32_t)sv.key[r]] = (float)(sv.w[r] / sw);
+    __syncthreads();
+    if (t == 0) {
+      uint32_t c1 = 0, c2 = 0;
+      for (uint32_t j = 0; j < n; ++j) {
+        if (sv.flag[j] >= 1) { if (c1 < a.cap) a.topk_ids[(size_t)row * a.cap + c1] = sv.idx[j]; ++c1; }
+        if (sv.flag[j] == 2) {
+          if (c2 < a.cap) {
+            a.keep_ids[(size_t)row * a.cap + c2] = sv.idx[j];
+            a.keep_probs[(size_t)row * a.cap + c2] = sv.e[j];
+          }
+          ++c2;
+        }
+      }
+      a.topk_count[row] = c1;
+      a.keep_count[row] = c2;
+    }
+  }
+}
+
+// ================================================================ moss-nano
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_nano(RowArgs a) {
+  __shared__ uint8_t s_seen[kMaxVocabReg];
+  __shared__ SurvLds sv;
+  __shared__ uint32_t s_hist[256];
+  __shared__ BlockScratch s;
+  __shared__ uint32_t s_out[4];
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  uint32_t bad = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && !__builtin_isfinite(x[i])) bad = 1u;
+  bad = block_or_u(bad, s);
+  if (bad) {  // nano/sampling.rs:24-27
+    finish_row(a, row, 0u, TC_ENONFINITE, 0u);
+    no_verify(a, row);
+    return;
+  }
+  // every history id must be inside the vocabulary (nano/sampling.rs:28-31)
+  const bool oob = build_seen(a, row, s_seen, s);
+  if (oob) {
+    finish_row(a, row, 0u, TC_EINVAL, 0u);
+    no_verify(a, row);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    float v = x[i];
+    if (s_seen[e0 + i]) v = v < 0.0f ? v * a.pen_f : v / a.pen_f;
+    x[i] = v / a.t_f;
+  }
+  // stable rank order: value descending (total_cmp), id ascending
+  const uint32_t K = (uint32_t)(a.top_k < V ? a.top_k : V);
+  uint32_t key[ITEMS];
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    key[i] = tkey(x[i]);
+    if ((vm >> i) & 1u) kmax = key[i] > kmax ? key[i] : kmax;
+  }
+  uint32_t kk = 0;
+  block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk);
+  const float threshold = untkey(kk);
+  // max of the row under total order = ranked[0]
+  {
+    uint32_t v = kmax;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) { uint32_t w = __shfl_xor(v, o); v = w > v ? w : v; }
+    if (lane_id() == 0) s.u[wave_id()] = v;
+    __syncthreads();
+    uint32_t r = 0;
+    for (int w = 0; w < num_waves(); ++w) r = s.u[w] > r ? s.u[w] : r;
+    __syncthreads();
+    kmax = r;
+  }
+  const float maximum = untkey(kmax);
+  uint32_t surv = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && !(x[i] < threshold)) surv |= 1u << i;
+  const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
+  if (n > (uint32_t)kSurvCap) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  for (uint32_t j = t; j < n; j += blockDim.x) {
+    sv.w[j] = tc_exp_d((double)(sv.val[j] - maximum));
+    sv.key[j] = ((uint64_t)(~tkey(sv.val[j])) << 32) | (uint64_t)j;
+  }
+  __syncthreads();
+  if (a.topk_count) {
+    if (t == 0) {
+      uint32_t c = 0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.w[j] > 0.0) { if (c < a.cap) a.topk_ids[(size_t)row * a.cap + c] = sv.idx[j]; ++c; }
+      a.topk_count[row] = c;
+    }
+  }
+  if (a.do_topp) {
+    sort_survivors(sv, n);
+    if (t == 0) {
+      double total = -0.0;
+      for (uint32_t j = 0; j < n; ++j) total += sv.w[j];
+      double cum = 0.0;
+      for (uint32_t r = 0; r < n; ++r) {
+        const uint32_t j = (uint32_t)sv.key[r];
+        if (cum > a.top_p_d) sv.w[j] = 0.0;
+        else cum += sv.w[j] / total;
+      }
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    double sw = -0.0;
+    for (uint32_t j = 0; j < n; ++j) sw += sv.w[j];
+    double draw = reinterpret_cast<const double*>(a.uniforms)[row] * sw;
+    uint32_t tok = 0;
+    int32_t st = TC_EDIST;
+    for (uint32_t j = 0; j < n; ++j) {
+      draw -= sv.w[j];
+      if (sv.w[j] > 0.0 && draw <= 0.0) { tok = sv.idx[j]; st = TC_OK; break; }
+    }
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = st;
+    if (a.out_flags) a.out_flags[row] = 0u;
+    if (a.keep_count) {
+      uint32_t c = 0;
+      for (uint32_t j = 0; j < n; ++j)
+        if (sv.w[j] > 0.0) {
+          if (c < a.cap) {
+            a.keep_ids[(size_t)row * a.cap + c] = sv.idx[j];
+            a.keep_probs[(size_t)row * a.cap + c] = (float)(sv.w[j] / sw);
+          }
+          ++c;
+        }
+      a.keep_count[row] = c;
+    }
+  }
+}
+
+// ================================================================ qwen building blocks
+__global__ void k_fill_u8(uint8_t* p, size_t n) {
+  for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < n; j += (size_t)gridDim.x * blockDim.x) p[j] = 0;
+}
+
+__global__ void k_penalty_ids_mask(const uint32_t* ids, size_t n, uint8_t* mask, int V) {
+  for (size_t j = blockIdx.x * (size_t)blockDim.x + threadIdx.x; j < n; j += (size_t)gridDim.x * blockDim.x) {
+    uint32_t id = ids[j];
+    if (id < (uint32_t)V) mask[id] = 1;
+  }
+}
+
+__global__ void k_apply_penalty(const float* in, float* out, int rows, int V, long long ld, const uint8_t* bmask,
+                                const float* fmask, float pen_f, float inv_pen) {
+  const size_t total = (size_t)rows * (size_t)V;
+  for (size_t k = blockIdx.x * (size_t)blockDim.x + threadIdx.x; k < total; k += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = k / (size_t)V, c = k % (size_t)V;
+    const size_t o = r * (size_t)ld + c;
+    float v = in[o];
+    const bool pen = bmask ? (bmask[c] != 0) : (fmask[c] > 0.0f);
+    out[o] = pen ? v * (v > 0.0f ? inv_pen : pen_f) : v;
+  }
+}
+
+__global__ void k_add_mask(const float* in, float* out, int rows, int V, long long ld, const float* mask) {
+  const size_t total = (size_t)rows * (size_t)V;
+  for (size_t k = blockIdx.x * (size_t)blockDim.x + threadIdx.x; k < total; k += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = k / (size_t)V, c = k % (size_t)V;
+    const size_t o = r * (size_t)ld + c;
+    out[o] = in[o] + mask[c];
+  }
+}
+
+__global__ void k_build_suppression(float* mask, int V, uint32_t eos) {
+  const int start = V >= 1024 ? V - 1024 : 0;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < V; i += gridDim.x * blockDim.x)
+    mask[i] = (i >= start && (uint32_t)i != eos) ? -__builtin_inff() : 0.0f;
+}
+
+__global__ void k_update_penalty_mask(float* mask, int V, const uint32_t* token) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const uint32_t id = *token;
+    if (id < (uint32_t)V) mask[id] = 1.0f;
+  }
+}
+
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(kMaxThreads) k_greedy(const InT* logits, long long ld, int V, uint32_t* out) {
+  __shared__ uint64_t s_best[kMaxWaves];
+  __shared__ uint32_t s_nan0;
+  const int row = blockIdx.x, t = threadIdx.x;
+  const InT* rp = logits + (size_t)row * (size_t)ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  uint64_t best = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u) || __builtin_isnan(x[i])) continue;
+    uint64_t k = ((uint64_t)ckey(x[i]) << 32) | (uint64_t)(~(uint32_t)(e0 + i));
+    best = k > best ? k : best;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint64_t other = __shfl_xor(best, o);
+    best = other > best ? other : best;
+  }
+  if (t == 0) s_nan0 = 0u;
+  if (lane_id() == 0) s_best[wave_id()] = best;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (e0 + i == 0 && __builtin_isnan(x[i])) s_nan0 = 1u;
+  __syncthreads();
+  if (t == 0) {
+    uint64_t b = 0;
+    for (int w = 0; w < num_waves(); ++w) b = s_best[w] > b ? s_best[w] : b;
+    out[row] = (b == 0 || s_nan0) ? 0u : ~(uint32_t)(b & 0xffffffffu);
+  }
+}
+
+}  // namespace tc
+
+// ====================================================================== C ABI
+struct tc_ctx {
+  int device;
+  size_t max_rows;
+  size_t max_vocab;
+  uint8_t* d_mask;  // [max_vocab] byte mask for tc_apply_repetition_penalty
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(TC_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+struct DeviceGuard {
+  int prev = -1;
+  bool changed = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) == hipSuccess && prev != dev && hipSetDevice(dev) == hipSuccess) changed = true;
+  }
+  ~DeviceGuard() {
+    if (changed) (void)hipSetDevice(prev);
+  }
+};
+
+// Block shape for a register-resident row: ITEMS per thread, threads a
+// multiple of 64 in [256, 1024].
+bool pick_shape(int V, int dtype, int* items, int* threads) {
+  const int pad = dtype == TC_BF16 ? 7 : 3;
+  for (int it : {8, 16}) {
+    int nt = (V + pad + it - 1) / it;
+    nt = (nt + 63) / 64 * 64;
+    if (nt < 256) nt = 256;
+    if (nt <= tc::kMaxThreads) {
+      *items = it;
+      *threads = nt;
+      return true;
+    }
+  }
+  return false;
+}
+
+#define TC_DEFINE_LAUNCH(NAME)                                                                   \
+  hipError_t launch_##NAME(int dtype, int items, int threads, int rows, hipStream_t st,          \
+                           const tc::RowArgs& a) {                                               \
+    dim3 g(rows), b(threads);                                                                    \
+    if (dtype == TC_F32) {                                                                       \
+      if (items == 8) hipLaunchKernelGGL((tc::NAME<float, 8>), g, b, 0, st, a);                  \
+      else hipLaunchKernelGGL((tc::NAME<float, 16>), g, b, 0, st, a);                            \
+    } else {                                                                                     \
+      if (items == 8) hipLaunchKernelGGL((tc::NAME<uint16_t, 8>), g, b, 0, st, a);               \
+      else hipLaunchKernelGGL((tc::NAME<uint16_t, 16>), g, b, 0, st, a);                         \
+    }                                                                                            \
+    return hipGetLastError();                                                                    \
+  }
+
+TC_DEFINE_LAUNCH(k_qwen)
+TC_DEFINE_LAUNCH(k_indextts)
+TC_DEFINE_LAUNCH(k_cosy)
+TC_DEFINE_LAUNCH(k_moss)
+TC_DEFINE_LAUNCH(k_nano)
+
+}  // namespace
+
+extern "C" {
+
+const char* tc_last_error(void) { return g_err.c_str(); }
+
+int tc_abi_version(void) { return TC_ABI_VERSION; }
+
+int tc_create(int device, size_t max_rows, size_t max_vocab, tc_ctx** out) {
+  if (!out) return fail(TC_EINVAL, "tc_create: out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device < 0 || device >= n) return fail(TC_EINVAL, "tc_create: device %d of %d", device, n);
+  if (max_vocab == 0 || max_vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_create: bad max_vocab");
+  DeviceGuard g(device);
+  tc_ctx* c = new tc_ctx{device, max_rows, max_vocab, nullptr};
+  e = hipMalloc(&c->d_mask, max_vocab);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(TC_ENOMEM, "hipMalloc(%zu): %s", max_vocab, hipGetErrorString(e));
+  }
+  *out = c;
+  return TC_OK;
+}
+
+void tc_destroy(tc_ctx* ctx) {
+  if (!ctx) return;
+  DeviceGuard g(ctx->device);
+  if (ctx->d_mask) (void)hipFree(ctx->d_mask);
+  delete ctx;
+}
+
+int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t rows,
+              size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+              const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
+              const tc_verify_out* verify, tc_stream stream) {
+  if (!ctx || !p) return fail(TC_EINVAL, "tc_sample: ctx/params is NULL");
+  if (rows == 0) return TC_OK;
+  if (!d_logits || !d_out_ids || !d_uniforms) return fail(TC_EINVAL, "tc_sample: NULL device pointer");
+  if (dtype != TC_F32 && dtype != TC_BF16) return fail(TC_EINVAL, "tc_sample: dtype %d", dtype);
+  if (vocab == 0) return fail(TC_EINVAL, "tc_sample: vocab is 0");
+  if (ld < vocab) return fail(TC_EINVAL, "tc_sample: ld %zu < vocab %zu", ld, vocab);
+  if (rows > (size_t)INT32_MAX || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_sample: shape too large");
+  const int V = (int)vocab;
+  tc::RowArgs a{};
+  a.logits = d_logits;
+  a.ld = (long long)ld;
+  a.V = V;
+  a.rows = (int)rows;
+  a.hist_off = d_hist_off;
+  a.hist_ids = d_hist_ids;
+  a.hist_mode = p->hist_mode;
+  a.pen_mask = p->d_pen_mask;
+  a.add_mask = p->d_add_mask;
+  a.uniforms = d_uniforms;
+  a.out_ids = d_out_ids;
+  a.out_status = d_out_status;
+  a.out_flags = d_out_flags;
+  if (verify && verify->cap) {
+    if (!verify->d_topk_count || !verify->d_topk_ids || !verify->d_keep_count || !verify->d_keep_ids ||
+        !verify->d_keep_probs)
+      return fail(TC_EINVAL, "tc_sample: incomplete verify outputs");
+    a.cap = verify->cap;
+    a.topk_count = verify->d_topk_count;
+    a.topk_ids = verify->d_topk_ids;
+    a.keep_count = verify->d_keep_count;
+    a.keep_ids = verify->d_keep_ids;
+    a.keep_probs = verify->d_keep_probs;
+  }
+  a.eos_id = p->eos_id;
+  a.exclude_id = p->exclude_id;
+  a.min_keep = (int)p->min_keep;
+  const bool need_hist = p->hist_mode != TC_HIST_MASK;
+  if (p->hist_mode < 0 || p->hist_mode > TC_HIST_MASK) return fail(TC_EINVAL, "tc_sample: hist_mode");
+  switch (p->variant) {
+    case TC_QWEN: {
+      a.do_pen = fabs(p->repetition_penalty - 1.0) >= 1e-9;
+      if (a.do_pen && need_hist && (!d_hist_off || !d_hist_ids))
+        return fail(TC_EINVAL, "tc_sample: penalty needs a history");
+      if (a.do_pen && !need_hist && !p->d_pen_mask) return fail(TC_EINVAL, "tc_sample: penalty mask is NULL");
+      a.pen_f = (float)p->repetition_penalty;
+      a.inv_pen = 1.0f / a.pen_f;
+      a.do_temp = (p->temperature != 1.0 && p->temperature > 0.0);
+      a.tmul = (float)(1.0 / p->temperature);
+      a.greedy = p->temperature < 0.01;
+      a.K = p->top_k > 0 ? (int)(p->top_k < vocab ? p->top_k : vocab) : 0;
+      a.do_topp = p->top_p < 1.0 && p->top_p > 0.0;
+      a.top_p_f = (float)p->top_p;
+      break;
+    }
+    case TC_COSY_RAS: {  // llm.rs:436-445
+      const float tp = (float)p->top_p, tau = p->ras_tau;
+      if (!isfinite(tp) || tp <= 0.0f || tp > 1.0f || p->top_k == 0 || p->ras_win == 0 || !isfinite(tau) ||
+          !(tau >= 0.0f && tau <= 1.0f))
+        return fail(TC_EINVAL, "invalid RAS sampling parameters");
+      if (!d_hist_off || !d_hist_ids) return fail(TC_EINVAL, "tc_sample: cosyvoice3 needs the decoded history");
+      a.top_k = (int)(p->top_k < (uint32_t)INT32_MAX ? p->top_k : (uint32_t)INT32_MAX);
+      a.top_p_f = tp;
+      a.ras_win = (int)p->ras_win;
+      a.ras_thresh = (float)p->ras_win * tau;
+      break;
+    }
+    case TC_INDEXTTS: {  // generation.rs:559-571
+      if (p->repetition_penalty <= 0.0) return fail(TC_EINVAL, "repetition_penalty must be > 0");
+      if (p->temperature <= 0.0) return fail(TC_EINVAL, "temperature must be > 0 when sampling");
+      a.do_pen = p->repetition_penalty != 1.0;
+      if (a.do_pen && (!d_hist_off || !d_hist_ids)) return fail(TC_EINVAL, "tc_sample: penalty needs a history");
+      a.pen_f = (float)p->repetition_penalty;
+      a.do_temp = p->temperature != 1.0;
+      a.t_f = (float)p->temperature;
+      if (p->top_k != 0) {
+        size_t k = p->top_k > p->min_keep ? p->top_k : p->min_keep;
+        if (k > vocab) k = vocab;
+        a.K = (int)k;
+      }
+      a.do_topp = p->top_p < 1.0;
+      a.top_p_d = p->top_p;
+      break;
+    }
+    case TC_MOSS: {
+      if (p->top_k == 0 && (float)p->temperature != 0.0f) return fail(TC_EINVAL, "moss: top_k must be >= 1");
+      if (p->exclude_id >= 0 && (size_t)p->exclude_id >= vocab) return fail(TC_EINVAL, "moss: exclude id out of range");
+      a.do_pen = d_hist_off && d_hist_ids;
+      a.pen_f = (float)p->repetition_penalty;
+      a.t_f = (float)p->temperature;
+      a.greedy = a.t_f == 0.0f;
+      a.top_k = (int)(p->top_k < vocab ? p->top_k : vocab);
+      a.top_p_d = p->top_p;
+      break;
+    }
+    case TC_MOSS_NANO: {
+      if (p->top_k == 0) return fail(TC_EINVAL, "nano: top_k must be >= 1");
+      a.pen_f = (float)p->repetition_penalty;
+      a.t_f = (float)p->temperature;
+      a.top_k = (int)(p->top_k < vocab ? p->top_k : vocab);
+      a.do_topp = p->top_p < 1.0;
+      a.top_p_d = p->top_p;
+      break;
+    }
+    default:
+      return fail(TC_EINVAL, "tc_sample: variant %d", p->variant);
+  }
+  int items = 0, threads = 0;
+  if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg)
+    return fail(TC_EUNSUPPORTED, "tc_sample: vocab %d exceeds the register-resident kernel", V);
+  if ((size_t)V > ctx->max_vocab) return fail(TC_EINVAL, "tc_sample: vocab %d > context max %zu", V, ctx->max_vocab);
+  DeviceGuard g(ctx->device);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (p->variant) {
+    case TC_QWEN: e = launch_k_qwen(dtype, items, threads, (int)rows, st, a); break;
+    case TC_COSY_RAS: e = launch_k_cosy(dtype, items, threads, (int)rows, st, a); break;
+    case TC_INDEXTTS: e = launch_k_indextts(dtype, items, threads, (int)rows, st, a); break;
+    case TC_MOSS: e = launch_k_moss(dtype, items, threads, (int)rows, st, a); break;
+    default: e = launch_k_nano(dtype, items, threads, (int)rows, st, a); break;
+  }
+  if (e != hipSuccess) return hip_fail(e, "tc_sample launch");
+  return TC_OK;
+}
+
+static int grid_for(size_t n) {
+  size_t g = (n + 255) / 256;
+  if (g > 4096) g = 4096;
+  return (int)(g ? g : 1);
+}
+
+int tc_apply_repetition_penalty(tc_ctx* ctx, const float* d_in, float* d_out, size_t rows, size_t vocab, size_t ld,
+                                const uint32_t* d_ids, size_t n_ids, double penalty, tc_stream stream) {
+  // the [V] byte mask lives in the context's workspace (one context per stream)
+  if (!ctx || !d_in || !d_out || (n_ids && !d_ids)) return fail(TC_EINVAL, "tc_apply_repetition_penalty: NULL pointer");
+  if (ld < vocab || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_apply_repetition_penalty: shape");
+  if (vocab > ctx->max_vocab) return fail(TC_EINVAL, "tc_apply_repetition_penalty: vocab %zu > context max %zu", vocab, ctx->max_vocab);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (fabs(penalty - 1.0) < 1e-9) {
+    if (d_in != d_out) {
+      hipError_t e = hipMemcpy2DAsync(d_out, ld * 4, d_in, ld * 4, vocab * 4, rows, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy2DAsync");
+    }
+    return TC_OK;
+  }
+  DeviceGuard g(ctx->device);
+  uint8_t* mask = ctx->d_mask;
+  hipLaunchKernelGGL(tc::k_fill_u8, dim3(grid_for(vocab)), dim3(256), 0, st, mask, vocab);
+  if (n_ids)
+    hipLaunchKernelGGL(tc::k_penalty_ids_mask, dim3(grid_for(n_ids)), dim3(256), 0, st, d_ids, n_ids, mask, (int)vocab);
+  const float pf = (float)penalty;
+  hipLaunchKernelGGL(tc::k_apply_penalty, dim3(grid_for(rows * vocab)), dim3(256), 0, st, d_in, d_out, (int)rows,
+                     (int)vocab, (long long)ld, (const uint8_t*)mask, (const float*)nullptr, pf, 1.0f / pf);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_apply_repetition_penalty");
+}
+
+int tc_apply_repetition_penalty_with_mask(const float* d_in, float* d_out, size_t rows, size_t vocab, size_t ld,
+                                          const float* d_mask, double penalty, tc_stream stream) {
+  if (!d_in || !d_out || !d_mask) return fail(TC_EINVAL, "tc_apply_repetition_penalty_with_mask: NULL pointer");
+  if (ld < vocab || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_apply_repetition_penalty_with_mask: shape");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (fabs(penalty - 1.0) < 1e-9) {
+    if (d_in != d_out) {
+      hipError_t e = hipMemcpy2DAsync(d_out, ld * 4, d_in, ld * 4, vocab * 4, rows, hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy2DAsync");
+    }
+    return TC_OK;
+  }
+  const float pf = (float)penalty;
+  hipLaunchKernelGGL(tc::k_apply_penalty, dim3(grid_for(rows * vocab)), dim3(256), 0, st, d_in, d_out, (int)rows,
+                     (int)vocab, (long long)ld, (const uint8_t*)nullptr, d_mask, pf, 1.0f / pf);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_apply_repetition_penalty_with_mask");
+}
+
+int tc_build_suppression_mask(float* d_mask, size_t vocab, uint32_t eos_id, tc_stream stream) {
+  if (!d_mask || vocab == 0 || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_build_suppression_mask: args");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tc::k_build_suppression, dim3(grid_for(vocab)), dim3(256), 0, st, d_mask, (int)vocab, eos_id);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_build_suppression_mask");
+}
+
+int tc_apply_token_suppression_with_mask(const float* d_in, float* d_out, size_t rows, size_t vocab, size_t ld,
+                                         const float* d_mask, tc_stream stream) {
+  if (!d_in || !d_out || !d_mask) return fail(TC_EINVAL, "tc_apply_token_suppression_with_mask: NULL pointer");
+  if (ld < vocab || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_apply_token_suppression_with_mask: shape");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tc::k_add_mask, dim3(grid_for(rows * vocab)), dim3(256), 0, st, d_in, d_out, (int)rows,
+                     (int)vocab, (long long)ld, d_mask);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_apply_token_suppression_with_mask");
+}
+
+int tc_update_penalty_mask(float* d_mask, size_t vocab, const uint32_t* d_token, tc_stream stream) {
+  if (!d_mask || !d_token || vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_update_penalty_mask: args");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(tc::k_update_penalty_mask, dim3(1), dim3(64), 0, st, d_mask, (int)vocab, d_token);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_update_penalty_mask");
+}
+
+int tc_greedy_sample(const void* d_logits, int dtype, size_t rows, size_t vocab, size_t ld, uint32_t* d_out_ids,
+                     tc_stream stream) {
+  if (!d_logits || !d_out_ids) return fail(TC_EINVAL, "tc_greedy_sample: NULL pointer");
+  if (rows == 0) return TC_OK;
+  if (vocab == 0 || ld < vocab || vocab > (size_t)INT32_MAX || rows > (size_t)INT32_MAX)
+    return fail(TC_EINVAL, "tc_greedy_sample: shape");
+  if (dtype != TC_F32 && dtype != TC_BF16) return fail(TC_EINVAL, "tc_greedy_sample: dtype");
+  int items, threads;
+  if (!pick_shape((int)vocab, dtype, &items, &threads))
+    return fail(TC_EUNSUPPORTED, "tc_greedy_sample: vocab %zu too large", vocab);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  dim3 g((unsigned)rows), b(threads);
+  if (dtype == TC_F32) {
+    if (items == 8) hipLaunchKernelGGL((tc::k_greedy<float, 8>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else hipLaunchKernelGGL((tc::k_greedy<float, 16>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+  } else {
+    if (items == 8) hipLaunchKernelGGL((tc::k_greedy<uint16_t, 8>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else hipLaunchKernelGGL((tc::k_greedy<uint16_t, 16>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+  }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_greedy_sample");
+}
+
+}  // extern "C"

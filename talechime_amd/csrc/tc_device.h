@@ -1,0 +1,317 @@
+// tc_device.h -- device building blocks for the row sampler kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tc_math.h"
+#include "_gen/expf_glibc_exc.inc"
+
+namespace tc {
+
+constexpr int kWave = 64;
+constexpr int kMaxThreads = 1024;
+constexpr int kMaxWaves = kMaxThreads / kWave;
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+
+// Unsigned key ordered like Rust's f32::total_cmp.
+__device__ __forceinline__ uint32_t tkey(float f) {
+  uint32_t b = f2u(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float untkey(uint32_t k) {
+  return u2f((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// Key ordered like IEEE `<` on non-NaN floats (-0 and +0 share a key).
+__device__ __forceinline__ uint32_t ckey(float f) { return f == 0.0f ? 0x80000000u : tkey(f); }
+
+// Rust f32::max / f64::max (NaN operands ignored).
+__device__ __forceinline__ float rmaxf(float a, float b) {
+  return __builtin_isnan(a) ? b : (__builtin_isnan(b) ? a : (a > b ? a : b));
+}
+__device__ __forceinline__ double rmaxd(double a, double b) {
+  return __builtin_isnan(a) ? b : (__builtin_isnan(b) ? a : (a > b ? a : b));
+}
+
+// ---------------------------------------------------------------- glibc expf
+// glibc's expf differs from the correctly rounded value only on the inputs in
+// tc_expf_exc_keys, all of which sit within TC_EXPF_BAND ulp of a rounding
+// midpoint; there it returns the neighbour on the far side of the midpoint.
+__device__ __noinline__ bool expf_is_exception(uint32_t b) {
+  uint32_t h = b >> 16;
+  uint32_t lo = tc_expf_exc_index[h], hi = tc_expf_exc_index[h + 1];
+  while (lo < hi) {
+    uint32_t mid = (lo + hi) >> 1;
+    uint32_t k = tc_expf_exc_keys[mid];
+    if (k == b) return true;
+    if (k < b) lo = mid + 1;
+    else hi = mid;
+  }
+  return false;
+}
+
+__device__ __forceinline__ float expf_glibc(float x) {
+  if (__builtin_isnan(x)) return x;
+  if (x < -104.0f) return 0.0f;
+  if (x > 88.72283935546875f) return __builtin_inff();
+  double y = tc_exp_d((double)x);
+  float r = (float)y;
+  if (tc_mid_dist(y, r) < TC_EXPF_BAND) {
+    if (expf_is_exception(f2u(x))) r = u2f(tc_toward(y, r));
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------- wave / block
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+__device__ __forceinline__ int num_waves() { return blockDim.x >> 6; }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = rmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = v + __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_sum_u(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_or_u(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    uint32_t t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+struct BlockScratch {
+  float f[kMaxWaves];
+  uint32_t u[kMaxWaves + 16];
+  double d[kMaxWaves];
+};
+
+// Max over the block (NaN ignored); every thread gets the result.
+__device__ float block_max(float v, BlockScratch& s) {
+  v = wave_max(v);
+  if (lane_id() == 0) s.f[wave_id()] = v;
+  __syncthreads();
+  float r = s.f[0];
+  for (int w = 1; w < num_waves(); ++w) r = rmaxf(r, s.f[w]);
+  __syncthreads();
+  return r;
+}
+
+// Sum over the block: in-thread order, then a butterfly inside each wave, then
+// the wave sums in wave order.  Deterministic for a fixed block shape.
+__device__ float block_sum(float v, BlockScratch& s) {
+  v = wave_sum(v);
+  if (lane_id() == 0) s.f[wave_id()] = v;
+  __syncthreads();
+  float r = s.f[0];
+  for (int w = 1; w < num_waves(); ++w) r = r + s.f[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ double block_max_d(double v, BlockScratch& s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = rmaxd(v, __shfl_xor(v, o));
+  if (lane_id() == 0) s.d[wave_id()] = v;
+  __syncthreads();
+  double r = s.d[0];
+  for (int w = 1; w < num_waves(); ++w) r = rmaxd(r, s.d[w]);
+  __syncthreads();
+  return r;
+}
+
+__device__ uint32_t block_sum_u(uint32_t v, BlockScratch& s) {
+  v = wave_sum_u(v);
+  if (lane_id() == 0) s.u[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = 0;
+  for (int w = 0; w < num_waves(); ++w) r += s.u[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ uint32_t block_or_u(uint32_t v, BlockScratch& s) {
+  v = wave_or_u(v);
+  if (lane_id() == 0) s.u[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = 0;
+  for (int w = 0; w < num_waves(); ++w) r |= s.u[w];
+  __syncthreads();
+  return r;
+}
+
+// Exclusive prefix sum over threads in thread order; *total gets the sum.
+__device__ uint32_t block_excl_scan(uint32_t v, BlockScratch& s, uint32_t* total) {
+  uint32_t inc = wave_incl_scan(v);
+  if (lane_id() == kWave - 1) s.u[wave_id()] = inc;
+  __syncthreads();
+  uint32_t off = 0, tot = 0;
+  for (int w = 0; w < num_waves(); ++w) {
+    uint32_t t = s.u[w];
+    if (w < wave_id()) off += t;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+// K-th largest (K >= 1) of the 32-bit keys selected by bit i of `sel`.
+// Four MSB-first 8-bit radix passes with LDS histograms.  Returns false when
+// fewer than K keys are selected.
+template <int ITEMS>
+__device__ bool block_kth_largest(const uint32_t (&key)[ITEMS], uint32_t sel, uint32_t K,
+                                  uint32_t* hist /*[256]*/, BlockScratch& s, uint32_t* out) {
+  uint32_t prefix = 0, pmask = 0;
+  const int t = threadIdx.x;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    for (int i = t; i < 256; i += blockDim.x) hist[i] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (((sel >> i) & 1u) && (key[i] & pmask) == prefix)
+        atomicAdd(&hist[(key[i] >> shift) & 255u], 1u);
+    __syncthreads();
+    // threads 0..255 hold bins 255..0; an inclusive scan gives the count of
+    // keys whose digit is >= the bin.
+    uint32_t v = t < 256 ? hist[255 - t] : 0u;
+    uint32_t inc = wave_incl_scan(v);
+    if (t < 256 && lane_id() == kWave - 1) s.u[wave_id()] = inc;
+    __syncthreads();
+    if (t < 256) {
+      uint32_t off = 0;
+      for (int w = 0; w < wave_id(); ++w) off += s.u[w];
+      uint32_t P = off + inc, Pex = P - v;
+      if (P >= K && Pex < K) {
+        s.u[kMaxWaves + 0] = 255u - (uint32_t)t;
+        s.u[kMaxWaves + 1] = K - Pex;
+      }
+      if (t == 255) s.u[kMaxWaves + 2] = P;
+    }
+    __syncthreads();
+    if (pass == 0 && s.u[kMaxWaves + 2] < K) {
+      __syncthreads();
+      return false;
+    }
+    uint32_t d = s.u[kMaxWaves + 0];
+    K = s.u[kMaxWaves + 1];
+    prefix |= d << shift;
+    pmask |= 255u << shift;
+    __syncthreads();
+  }
+  *out = prefix;
+  return true;
+}
+
+// In-place ascending bitonic sort of n_pad (a power of two) 64-bit keys in LDS.
+__device__ void block_bitonic_sort(uint64_t* a, int n_pad) {
+  for (int k = 2; k <= n_pad; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < n_pad; i += blockDim.x) {
+        int ixj = i ^ j;
+        if (ixj > i) {
+          uint64_t x = a[i], y = a[ixj];
+          bool up = (i & k) == 0;
+          if ((x > y) == up) {
+            a[i] = y;
+            a[ixj] = x;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__device__ __forceinline__ int next_pow2(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// ---------------------------------------------------------------- row loads
+// Thread t holds the ITEMS consecutive elements e = t*ITEMS + i - shift of the
+// row, where `shift` aligns the row start down to 16 bytes.  Only 16-byte
+// chunks that contain at least one element of the row are read; a 16-byte
+// aligned chunk never crosses a page, so no read can fault.  Elements outside
+// [0, V) are reported invalid.
+template <int ITEMS>
+__device__ __forceinline__ void load_row(const float* row, int V, float (&x)[ITEMS], int* shift_out) {
+  static_assert(ITEMS % 4 == 0, "f32 rows load 4 elements per 16 bytes");
+  const int shift = (int)((reinterpret_cast<uintptr_t>(row) >> 2) & 3u);
+  const float4* base = reinterpret_cast<const float4*>(row - shift);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int c = 0; c < ITEMS / 4; ++c) {
+    const int q = t * (ITEMS / 4) + c;
+    const int e0 = q * 4 - shift;
+    if (e0 + 3 >= 0 && e0 < V) {
+      float4 v = base[q];
+      x[4 * c + 0] = v.x;
+      x[4 * c + 1] = v.y;
+      x[4 * c + 2] = v.z;
+      x[4 * c + 3] = v.w;
+    } else {
+      x[4 * c + 0] = x[4 * c + 1] = x[4 * c + 2] = x[4 * c + 3] = -__builtin_inff();
+    }
+  }
+  *shift_out = shift;
+}
+
+template <int ITEMS>
+__device__ __forceinline__ void load_row(const uint16_t* row, int V, float (&x)[ITEMS], int* shift_out) {
+  static_assert(ITEMS % 8 == 0, "bf16 rows load 8 elements per 16 bytes");
+  const int shift = (int)((reinterpret_cast<uintptr_t>(row) >> 1) & 7u);
+  const uint4* base = reinterpret_cast<const uint4*>(row - shift);
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int c = 0; c < ITEMS / 8; ++c) {
+    const int q = t * (ITEMS / 8) + c;
+    const int e0 = q * 8 - shift;
+    if (e0 + 7 >= 0 && e0 < V) {
+      uint4 v = base[q];
+      uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        x[8 * c + 2 * j + 0] = u2f(w[j] << 16);
+        x[8 * c + 2 * j + 1] = u2f(w[j] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[8 * c + j] = -__builtin_inff();
+    }
+  }
+  *shift_out = shift;
+}
+
+template <int ITEMS>
+__device__ __forceinline__ uint32_t valid_mask(int V, int shift) {
+  uint32_t m = 0;
+  const int e0 = (int)threadIdx.x * ITEMS - shift;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (e0 + i >= 0 && e0 + i < V) m |= 1u << i;
+  return m;
+}
+
+}  // namespace tc

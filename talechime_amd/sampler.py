@@ -1,0 +1,144 @@
+"""Batched device sampler: torch tensors in, token ids out, through the C ABI.
+
+``DeviceSampler.sample`` is the one entry every host-side mirror
+(qwen / cosyvoice3 / indextts / moss) goes through.  Tensors must already be on
+the GPU; nothing is copied to the host unless the caller asks for it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import (BF16, COSY_RAS, F32, HIST_MASK, HIST_PER_ROW, INDEXTTS, MOSS, MOSS_NANO, QWEN,
+                   SampleParams, TcError, VerifyOut, check, load)
+
+__all__ = ["DeviceSampler", "make_params", "SampleResult", "QWEN", "COSY_RAS", "INDEXTTS", "MOSS",
+           "MOSS_NANO", "TcError"]
+
+
+def make_params(variant: int, *, temperature: float = 1.0, top_p: float = 1.0, penalty: float = 1.0,
+                top_k: int = 0, min_keep: int = 2, ras_win: int = 10, ras_tau: float = 0.1,
+                eos_id: int = -1, exclude_id: int = -1, hist_mode: int = HIST_PER_ROW,
+                add_mask: torch.Tensor | None = None, pen_mask: torch.Tensor | None = None) -> SampleParams:
+    p = SampleParams()
+    p.variant, p.hist_mode = variant, hist_mode
+    p.temperature, p.top_p, p.repetition_penalty = float(temperature), float(top_p), float(penalty)
+    p.top_k, p.min_keep, p.ras_win, p.ras_tau = int(top_k), int(min_keep), int(ras_win), float(ras_tau)
+    p.eos_id, p.exclude_id = int(eos_id), int(exclude_id)
+    if add_mask is not None:
+        _need_cuda(add_mask, torch.float32, "add_mask")
+        p.d_add_mask = add_mask.data_ptr()
+    if pen_mask is not None:
+        _need_cuda(pen_mask, torch.float32, "pen_mask")
+        p.d_pen_mask = pen_mask.data_ptr()
+    p._keep = (add_mask, pen_mask)  # keep the tensors alive with the struct
+    return p
+
+
+def _need_cuda(t: torch.Tensor, dtype, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+@dataclass
+class SampleResult:
+    ids: torch.Tensor            # [rows] int32 (u32 bits)
+    status: torch.Tensor         # [rows] int32
+    flags: torch.Tensor          # [rows] int32
+    topk_count: torch.Tensor | None = None
+    topk_ids: torch.Tensor | None = None
+    keep_count: torch.Tensor | None = None
+    keep_ids: torch.Tensor | None = None
+    keep_probs: torch.Tensor | None = None
+
+
+class DeviceSampler:
+    """Owns one tc_ctx (the library's workspace) on one GPU."""
+
+    def __init__(self, device: int | None = None, max_rows: int = 4096, max_vocab: int = 1 << 18):
+        L = load()
+        self.device = torch.cuda.current_device() if device is None else int(device)
+        self._ctx = C.c_void_p()
+        check(L.tc_create(self.device, max_rows, max_vocab, C.byref(self._ctx)))
+        self.max_vocab = max_vocab
+
+    def close(self) -> None:
+        if self._ctx:
+            load().tc_destroy(self._ctx)
+            self._ctx = C.c_void_p()
+
+    def __del__(self):  # pragma: no cover - interpreter shutdown order
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def ctx(self) -> C.c_void_p:
+        return self._ctx
+
+    def sample(self, params: SampleParams, logits: torch.Tensor, hist_off: torch.Tensor | None,
+               hist_ids: torch.Tensor | None, uniforms: torch.Tensor, *, verify_cap: int = 0,
+               stream: torch.cuda.Stream | None = None, out: SampleResult | None = None) -> SampleResult:
+        if logits.dim() != 2 or logits.stride(1) != 1 or not logits.is_cuda:
+            raise ValueError("logits must be a 2-D GPU tensor with unit stride in the vocab dim")
+        if logits.dtype == torch.float32:
+            dt = F32
+        elif logits.dtype == torch.bfloat16:
+            dt = BF16
+        else:
+            raise ValueError(f"logits dtype {logits.dtype} (f32 or bf16 expected)")
+        rows, V = logits.shape
+        dev = logits.device
+        need_u = torch.float64 if params.variant in (INDEXTTS, MOSS, MOSS_NANO) else torch.float32
+        _need_cuda(uniforms, need_u, "uniforms")
+        per_row = 2 if params.variant == COSY_RAS else 1
+        if uniforms.numel() < rows * per_row:
+            raise ValueError("not enough uniforms")
+        ho = hi = None
+        if hist_off is not None:
+            _need_cuda(hist_off, None, "hist_off")
+            _need_cuda(hist_ids, None, "hist_ids")
+            if hist_off.element_size() != 4 or hist_ids.element_size() != 4:
+                raise ValueError("history tensors must hold 32-bit ids")
+            if params.hist_mode == HIST_PER_ROW and hist_off.numel() < rows + 1:
+                raise ValueError("hist_off needs rows + 1 entries")
+            ho, hi = hist_off.data_ptr(), hist_ids.data_ptr() if hist_ids.numel() else hist_off.data_ptr()
+        if out is None:
+            out = SampleResult(torch.empty(rows, dtype=torch.int32, device=dev),
+                               torch.empty(rows, dtype=torch.int32, device=dev),
+                               torch.empty(rows, dtype=torch.int32, device=dev))
+        ver = None
+        if verify_cap:
+            out.topk_count = torch.zeros(rows, dtype=torch.int32, device=dev)
+            out.topk_ids = torch.zeros(rows, verify_cap, dtype=torch.int32, device=dev)
+            out.keep_count = torch.zeros(rows, dtype=torch.int32, device=dev)
+            out.keep_ids = torch.zeros(rows, verify_cap, dtype=torch.int32, device=dev)
+            out.keep_probs = torch.zeros(rows, verify_cap, dtype=torch.float32, device=dev)
+            ver = VerifyOut(verify_cap, out.topk_count.data_ptr(), out.topk_ids.data_ptr(),
+                            out.keep_count.data_ptr(), out.keep_ids.data_ptr(), out.keep_probs.data_ptr())
+        st = (stream or torch.cuda.current_stream(dev)).cuda_stream
+        rc = load().tc_sample(self._ctx, C.byref(params), logits.data_ptr(), dt, rows, V, logits.stride(0),
+                              ho, hi, uniforms.data_ptr(), out.ids.data_ptr(), out.status.data_ptr(),
+                              out.flags.data_ptr(), C.byref(ver) if ver is not None else None, st)
+        check(rc)
+        return out
+
+
+def launch_shape(vocab: int, dtype: int = F32) -> tuple[int, int]:
+    """(items per thread, threads per block) the library uses for one row of
+    ``vocab`` logits (mirrors pick_shape in csrc/sampler.hip)."""
+    pad = 7 if dtype == BF16 else 3
+    for items in (8, 16):
+        nt = -(-(vocab + pad) // items)
+        nt = max(256, -(-nt // 64) * 64)
+        if nt <= 1024:
+            return items, nt
+    raise ValueError(f"vocab {vocab} exceeds the register-resident kernel")

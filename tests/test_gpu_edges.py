@@ -1,0 +1,337 @@
+"""Edge cases and reference known-answer rows through the HIP sampler, each
+checked against the oracle on identical inputs (ties, -inf/NaN/+inf rows, k
+larger than V, greedy, misaligned and padded rows, bf16, penalty modes,
+suppression and EOS masks, error statuses)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from talechime_amd import _lib  # noqa: E402
+from talechime_amd.sampler import DeviceSampler, launch_shape, make_params  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+NEG = -np.inf
+CAP = 64
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    s = DeviceSampler(0, max_rows=4096, max_vocab=1 << 18)
+    yield s
+    s.close()
+
+
+def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=False, dev_order=True,
+        hist_mode=0, add_mask=None, pen_mask=None, **kw):
+    """Sample with both the GPU and the oracle; returns (gpu dict, oracle dict)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    rows, V = x.shape
+    if hist is None:
+        hist = [[] for _ in range(rows)]
+    if hist_mode == 1:
+        off = np.array([0, len(hist[0])], np.uint32)
+        ids = np.asarray(hist[0], np.uint32)
+    else:
+        off = np.zeros(rows + 1, np.uint32)
+        off[1:] = np.cumsum([len(h) for h in hist])
+        ids = np.concatenate([np.asarray(h, np.uint32) for h in hist]) if off[-1] else np.zeros(0, np.uint32)
+    f64 = variant in (O.INDEXTTS, O.MOSS, O.MOSS_NANO)
+    per = 2 if variant == O.COSY_RAS else 1
+    u = np.asarray(uniforms, np.float64 if f64 else np.float32).reshape(-1)
+    assert u.size >= rows * per
+    # device copy, optionally padded rows (ld > V) and bf16
+    ld = V + ld_pad
+    if bf16:
+        bits = np.zeros((rows, ld), np.uint16)
+        from talechime_amd.synth import bf16_bits_to_f32, to_bf16_bits
+        bits[:, :V] = to_bf16_bits(x)
+        x = bf16_bits_to_f32(bits[:, :V]).copy()
+        dl = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda()[:, :V]
+    else:
+        buf = np.zeros((rows, ld), np.float32)
+        buf[:, :V] = x
+        dl = torch.from_numpy(buf).cuda()[:, :V]
+    dho = torch.from_numpy(off.view(np.int32).copy()).cuda()
+    dhi = torch.from_numpy((ids if ids.size else np.zeros(1, np.uint32)).view(np.int32).copy()).cuda()
+    du = torch.from_numpy(u).cuda()
+    am = torch.from_numpy(np.asarray(add_mask, np.float32)).cuda() if add_mask is not None else None
+    pm = torch.from_numpy(np.asarray(pen_mask, np.float32)).cuda() if pen_mask is not None else None
+    p = make_params(variant, hist_mode=hist_mode, add_mask=am, pen_mask=pm, **kw)
+    r = sampler.sample(p, dl, dho, dhi, du, verify_cap=CAP)
+    torch.cuda.synchronize()
+    g = {k: getattr(r, k).cpu().numpy() for k in ("ids", "status", "flags", "topk_count", "topk_ids",
+                                                  "keep_count", "keep_ids", "keep_probs")}
+    g["ids"] = g["ids"].view(np.uint32)
+    dord = None
+    if dev_order and variant in (O.COSY_RAS, O.INDEXTTS):
+        items, threads = launch_shape(V, 1 if bf16 else 0)
+        dord = (items, threads, 8 if bf16 else 4, ld)
+    okw = dict(kw)
+    okw["penalty"] = okw.pop("penalty", 1.0)
+    op = O.make_params(variant, hist_mode=hist_mode, add_mask=add_mask, pen_mask=pen_mask,
+                       dev_order=dord, **okw)
+    o = O.sample(op, x, off, ids, u, cap=CAP)
+    return g, o
+
+
+def same(g, o, rows=None, probs_exact=True):
+    rows = range(g["ids"].size) if rows is None else rows
+    for r in rows:
+        if o["status"][r] != 0:
+            assert g["status"][r] == o["status"][r], (r, g["status"][r], o["status"][r])
+            continue
+        assert g["status"][r] == 0, (r, g["status"][r])
+        assert g["ids"][r] == o["ids"][r], (r, g["ids"][r], o["ids"][r])
+        assert g["flags"][r] == o["flags"][r], (r, g["flags"][r], o["flags"][r])
+        for c, i in (("topk_count", "topk_ids"), ("keep_count", "keep_ids")):
+            assert g[c][r] == o[c][r], (r, c, g[c][r], o[c][r])
+            n = min(int(g[c][r]), CAP)
+            assert np.array_equal(g[i][r, :n].astype(np.uint32), o[i][r, :n]), (r, i)
+        n = min(int(g["keep_count"][r]), CAP)
+        if probs_exact:
+            assert np.array_equal(g["keep_probs"][r, :n], o["keep_probs"][r, :n]), r
+        else:
+            np.testing.assert_allclose(g["keep_probs"][r, :n], o["keep_probs"][r, :n], rtol=1e-5)
+
+
+QWEN_KW = dict(temperature=0.7, top_k=50, top_p=0.9)
+
+
+# ------------------------------------------------------------------ qwen
+@pytest.mark.parametrize("vocab", [4, 3072])
+def test_qwen_device_parity_template(sampler, vocab):
+    # crates/qwen3-tts/src/generation/sampling.rs:873-900
+    row = np.full(vocab, NEG, np.float32)
+    for i, v in ((vocab - 1, 2.0), (vocab // 2, 1.0), (1, 1.0)):
+        row[i] = v
+    for top_p in (0.5, 0.7, 0.9):
+        for seed in range(16):
+            u = [O.QwenRng(seed).rand_f32()]
+            g, o = run(sampler, O.QWEN, [row], uniforms=u, temperature=0.7, top_k=3, top_p=top_p)
+            same(g, o)
+
+
+def test_qwen_reference_rows(sampler):
+    # sampling.rs:493-506, 692-705 (greedy), 789-804, 818-848
+    g, o = run(sampler, O.QWEN, [[1.0, 10.0, 2.0, 1.0]], uniforms=[0.3], temperature=0.001, top_k=50, top_p=0.9)
+    assert g["ids"][0] == 1 and g["flags"][0] == _lib.FLAG_GREEDY
+    g, o = run(sampler, O.QWEN, [[10.0, 1.0, 1.0], [1.0, 10.0, 1.0]], uniforms=[0.3, 0.3], temperature=0.001,
+               top_k=50, top_p=0.9)
+    assert g["ids"].tolist() == [0, 1]
+    g, o = run(sampler, O.QWEN, [[1.0, 5.0, 3.0, 2.0, 4.0, 4.0]], uniforms=[0.99], temperature=1.0, top_k=3,
+               top_p=0.9)
+    same(g, o)
+    assert sorted(g["topk_ids"][0, :3].tolist()) == [1, 4, 5]
+    sparse = np.full(3072, NEG, np.float32)
+    for i, v in ((1001, 4.0), (500, 3.0), (2000, 2.0), (100, 1.0)):
+        sparse[i] = v
+    g, o = run(sampler, O.QWEN, [sparse], uniforms=[0.5], temperature=1.0, top_k=0, top_p=0.8)
+    same(g, o)
+    assert g["keep_ids"][0, :2].tolist() == [500, 1001]
+
+
+def test_qwen_ties_and_degenerate_rows(sampler):
+    rows = [
+        np.zeros(64, np.float32),                     # all equal: ties at top-k and top-p
+        np.full(64, NEG, np.float32),                 # all -inf -> index 0
+        np.r_[np.float32(np.inf), np.zeros(63, np.float32)],  # +inf -> NaN CDF -> index 0
+        np.arange(64, dtype=np.float32) % 4,          # repeated values
+    ]
+    for u in (0.0, 0.37, 1.0):
+        for k, p in ((5, 0.5), (64, 0.95), (100, 0.3), (1, 0.9), (0, 0.6)):
+            g, o = run(sampler, O.QWEN, rows, uniforms=[u] * 4, temperature=1.0, top_k=k, top_p=p)
+            tie = (o["flags"] & 1) != 0
+            same(g, o, rows=[r for r in range(4) if not tie[r]])
+
+
+def test_qwen_greedy_nan_and_ties(sampler):
+    rows = np.array([[np.nan, 5.0, 5.0, 1.0], [1.0, 5.0, 5.0, np.nan], [-0.0, 0.0, -1.0, -2.0]], np.float32)
+    g, o = run(sampler, O.QWEN, rows, uniforms=[0.5] * 3, temperature=0.001, top_k=0, top_p=1.0)
+    assert g["ids"].tolist() == o["ids"].tolist() == [0, 1, 0]
+
+
+@pytest.mark.parametrize("ld_pad", [0, 1, 2, 3, 5])
+@pytest.mark.parametrize("V", [2, 100, 2049, 5000, 8194, 16000])
+def test_qwen_shapes_and_alignment(sampler, V, ld_pad):
+    g_ = np.random.default_rng(V * 10 + ld_pad)
+    rows = 5
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    hist = [g_.integers(0, V + 5, 40).tolist() for _ in range(rows)]  # some ids >= V
+    u = [O.QwenRng(V + ld_pad).rand_f32() for _ in range(rows)]
+    g, o = run(sampler, O.QWEN, x, hist, u, ld_pad=ld_pad, temperature=0.9, top_k=50, top_p=0.8, penalty=1.3)
+    tie = (o["flags"] & 1) != 0
+    same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+def test_qwen_bf16(sampler):
+    g_ = np.random.default_rng(5)
+    V = 3000
+    x = (g_.standard_normal((6, V)) * 3).astype(np.float32)
+    u = [O.QwenRng(1).rand_f32() for _ in range(6)]
+    for pad in (0, 1, 3):
+        g, o = run(sampler, O.QWEN, x, None, u, bf16=True, ld_pad=pad, temperature=0.7, top_k=40, top_p=0.95)
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(6) if not tie[r]])
+
+
+def test_qwen_penalty_modes_and_masks(sampler):
+    g_ = np.random.default_rng(9)
+    V, rows = 3072, 4
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    hist = [g_.integers(0, V, 100).tolist()]
+    u = [O.QwenRng(3).rand_f32() for _ in range(rows)]
+    sup = O.qwen_suppression_mask(V, 2150)
+    # broadcast history (apply_repetition_penalty semantics) + suppression + EOS
+    g, o = run(sampler, O.QWEN, x, hist, u, hist_mode=1, add_mask=sup, eos_id=2150, temperature=0.9, top_k=50,
+               top_p=0.9, penalty=1.05)
+    same(g, o)
+    assert all(i < 2048 for i in g["ids"])
+    # mask mode (apply_repetition_penalty_with_mask)
+    mask = np.zeros(V, np.float32)
+    mask[g_.integers(0, V, 200)] = 1.0
+    g, o = run(sampler, O.QWEN, x, None, u, hist_mode=2, pen_mask=mask, temperature=0.9, top_k=50, top_p=0.9,
+               penalty=2.0)
+    same(g, o)
+
+
+# ------------------------------------------------------------------ indextts
+def test_indextts_random_rows(sampler):
+    g_ = np.random.default_rng(11)
+    for V in (5, 300, 8194):
+        x = (g_.standard_normal((8, V)) * 4).astype(np.float32)
+        x[0, :3] = x[0, 3]  # ties at the top
+        hist = [g_.integers(0, V, 60).tolist() for _ in range(8)]
+        u = g_.random(8)
+        for k, p in ((30, 0.8), (2, 0.5), (0, 0.9), (V + 5, 0.99), (30, 1.0)):
+            g, o = run(sampler, O.INDEXTTS, x, hist, u, temperature=0.8, top_k=k, top_p=p, penalty=10.0, min_keep=2)
+            if V > 1024 and (k == 0 or k >= V):
+                # more than 1024 survivors: not implemented by the LDS-resident kernel
+                assert (g["status"] == _lib.TC_EUNSUPPORTED).all()
+                continue
+            same(g, o)
+
+
+def test_indextts_nan_row_too_few(sampler):
+    x = np.array([[0.0, np.nan, 1.0, 2.0]], np.float32)
+    g, o = run(sampler, O.INDEXTTS, x, None, [0.5], temperature=0.8, top_k=30, top_p=0.8, penalty=1.0)
+    assert o["status"][0] == O.ETOOFEW and g["status"][0] == _lib.TC_ETOOFEW
+
+
+# ------------------------------------------------------------------ cosyvoice3
+def test_cosy_ignore_eos(sampler):
+    # crates/cosyvoice3/src/llm.rs:713-735
+    vocab, eos = 6761, 6561
+    raw = np.full((1, vocab), -20.0, np.float32)
+    raw[0, eos], raw[0, 7] = 50.0, 10.0
+    rng = O.StepRng(42)
+    kw = dict(top_p=0.9, top_k=5, ras_win=10, ras_tau=0.1)
+    g, o = run(sampler, O.COSY_RAS, raw, [[]], [rng.next_f32(), 0.0], eos_id=eos, **kw)
+    assert g["ids"][0] == o["ids"][0] == 7
+    g, o = run(sampler, O.COSY_RAS, raw, [[]], [rng.next_f32(), 0.0], eos_id=-1, **kw)
+    assert g["ids"][0] == o["ids"][0] == eos
+
+
+def test_cosy_random_rows_and_ras(sampler):
+    g_ = np.random.default_rng(12)
+    V = 700
+    x = (g_.standard_normal((10, V)) * 3).astype(np.float32)
+    x[:, 5] += 20.0
+    hist = [([5] if r % 2 else [1]) + g_.integers(0, V, 5).tolist() for r in range(10)]
+    u = g_.random(20).astype(np.float32)
+    g, o = run(sampler, O.COSY_RAS, x, hist, u, top_p=0.8, top_k=25, ras_win=10, ras_tau=0.1)
+    same(g, o)
+    assert ((g["flags"] & 2) != 0).sum() >= 4
+
+
+def test_cosy_invalid_params(sampler):
+    x = np.zeros((1, 8), np.float32)
+    with pytest.raises(_lib.TcError) as e:
+        run(sampler, O.COSY_RAS, x, [[]], [0.5, 0.5], top_p=0.0, top_k=25, ras_win=10, ras_tau=0.1)
+    assert e.value.code == _lib.TC_EINVAL
+
+
+# ------------------------------------------------------------------ moss / nano
+def test_moss_rows(sampler):
+    g_ = np.random.default_rng(13)
+    V = 1027
+    x = (g_.standard_normal((16, V)) * 2).astype(np.float32)
+    hist = [g_.integers(0, V, 30).tolist() for _ in range(16)]
+    u = g_.random(16)
+    for T, k, p, ex in ((0.8, 30, 0.6, -1), (1.7, 25, 0.8, 1026), (0.0, 30, 0.6, -1), (1.0, 1000, 0.99, 3)):
+        g, o = run(sampler, O.MOSS, x, hist, u, temperature=T, top_k=k, top_p=p, penalty=1.1, exclude_id=ex)
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(16) if not tie[r]], probs_exact=False)
+    bad = x[:2].copy()
+    bad[0, 3] = np.nan
+    bad[1, :] = NEG
+    g, o = run(sampler, O.MOSS, bad, None, [0.5, 0.5], temperature=0.8, top_k=30, top_p=0.6, penalty=1.0)
+    assert g["status"].tolist() == [_lib.TC_ENONFINITE] * 2
+
+
+def test_nano_reference_rows(sampler):
+    # crates/moss-tts/src/nano/sampling.rs:82-99
+    u = [O.NanoLcg(42).next_unit()]
+    x = [[0.0, 1.0, 2.0, 3.0]]
+    g, _ = run(sampler, O.MOSS_NANO, x, [[]], u, temperature=1.0, top_k=4, top_p=1.0, penalty=1.0)
+    assert g["ids"][0] == 2
+    g, _ = run(sampler, O.MOSS_NANO, x, [[]], u, temperature=1.0, top_k=4, top_p=0.5, penalty=1.0)
+    assert g["ids"][0] == 3
+    g, _ = run(sampler, O.MOSS_NANO, x, [[3, 3, 3]], u, temperature=1.0, top_k=1, top_p=1.0, penalty=2.0)
+    assert g["ids"][0] == 2
+    g, _ = run(sampler, O.MOSS_NANO, [[np.nan]], [[]], u, temperature=1.0, top_k=1, top_p=1.0, penalty=1.0)
+    assert g["status"][0] == _lib.TC_ENONFINITE
+    g, _ = run(sampler, O.MOSS_NANO, [[0.0, 1.0]], [[5]], u, temperature=1.0, top_k=1, top_p=1.0, penalty=2.0)
+    assert g["status"][0] == _lib.TC_EINVAL
+
+
+def test_nano_rows(sampler):
+    g_ = np.random.default_rng(14)
+    V = 1024
+    x = (g_.standard_normal((16, V)) * 2).astype(np.float32)
+    hist = [g_.integers(0, V, 20).tolist() for _ in range(16)]
+    lcg = O.NanoLcg(7)
+    u = [lcg.next_unit() for _ in range(16)]
+    for T, k, p in ((0.8, 25, 0.95), (1.0, 2, 1.0), (1.3, 1024, 0.5)):
+        g, o = run(sampler, O.MOSS_NANO, x, hist, u, temperature=T, top_k=k, top_p=p, penalty=1.2)
+        same(g, o, probs_exact=False)
+
+
+# ------------------------------------------------------------------ building blocks
+def test_building_blocks(sampler):
+    L = _lib.load()
+    g_ = np.random.default_rng(15)
+    V, rows = 3072, 3
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    ids = g_.integers(0, V + 10, 80).astype(np.uint32)
+    dx = torch.from_numpy(x).cuda()
+    dout = torch.empty_like(dx)
+    dids = torch.from_numpy(ids.view(np.int32)).cuda()
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(L.tc_apply_repetition_penalty(sampler.ctx, dx.data_ptr(), dout.data_ptr(), rows, V, V,
+                                             dids.data_ptr(), ids.size, 1.05, st))
+    torch.cuda.synchronize()
+    assert np.array_equal(dout.cpu().numpy(), O.qwen_penalty_ids(x, ids, 1.05))
+    mask = torch.zeros(V, dtype=torch.float32, device="cuda")
+    _lib.check(L.tc_build_suppression_mask(mask.data_ptr(), V, 2150, st))
+    torch.cuda.synchronize()
+    assert np.array_equal(mask.cpu().numpy(), O.qwen_suppression_mask(V, 2150))
+    _lib.check(L.tc_apply_token_suppression_with_mask(dx.data_ptr(), dout.data_ptr(), rows, V, V,
+                                                      mask.data_ptr(), st))
+    torch.cuda.synchronize()
+    assert np.array_equal(dout.cpu().numpy(), O.qwen_add_mask(x, O.qwen_suppression_mask(V, 2150)))
+    pm = torch.zeros(V, dtype=torch.float32, device="cuda")
+    tok = torch.tensor([17], dtype=torch.int32, device="cuda")
+    _lib.check(L.tc_update_penalty_mask(pm.data_ptr(), V, tok.data_ptr(), st))
+    _lib.check(L.tc_apply_repetition_penalty_with_mask(dx.data_ptr(), dout.data_ptr(), rows, V, V,
+                                                       pm.data_ptr(), 2.0, st))
+    torch.cuda.synchronize()
+    want = O.qwen_penalty_mask(x, pm.cpu().numpy(), 2.0)
+    assert pm.cpu().numpy()[17] == 1.0 and np.array_equal(dout.cpu().numpy(), want)
+    out = torch.empty(rows, dtype=torch.int32, device="cuda")
+    _lib.check(L.tc_greedy_sample(dx.data_ptr(), 0, rows, V, V, out.data_ptr(), st))
+    torch.cuda.synchronize()
+    assert out.cpu().numpy().tolist() == [O.argmax(r) for r in x]
