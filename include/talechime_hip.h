@@ -106,7 +106,10 @@ typedef struct tc_sample_params {
 
 /* Optional verification outputs (device pointers; pass NULL to skip).  Ids are
  * ascending; keep_probs holds the probability the draw used for each kept id
- * (f64 variants are rounded to float).  Counts are exact even when > cap. */
+ * (f64 variants are rounded to float).  Counts are exact even when > cap.
+ * d_norm (may be NULL) receives the row's normaliser: the log-sum of the
+ * indextts log_softmax, the softmax denominator for qwen and cosyvoice3, NaN
+ * where the row has none. */
 typedef struct tc_verify_out {
   uint32_t cap;
   uint32_t* d_topk_count;  /* [rows] */
@@ -114,6 +117,7 @@ typedef struct tc_verify_out {
   uint32_t* d_keep_count;  /* [rows] */
   uint32_t* d_keep_ids;    /* [rows * cap] final candidates */
   float* d_keep_probs;     /* [rows * cap] */
+  float* d_norm;           /* [rows] */
 } tc_verify_out;
 
 /* Create a context on `device` for batches up to max_rows x max_vocab.  The

@@ -53,6 +53,7 @@ class Verify(C.Structure):
         ("keep_count", C.c_void_p),
         ("keep_ids", C.c_void_p),
         ("keep_probs", C.c_void_p),
+        ("norm", C.c_void_p),
     ]
 
 
@@ -342,10 +343,10 @@ def sample(params, logits, hist_off=None, hist_ids=None, uniforms=None, *, cap=0
         res = {
             "topk_count": np.zeros(rows, np.uint32), "topk_ids": np.zeros((rows, cap), np.uint32),
             "keep_count": np.zeros(rows, np.uint32), "keep_ids": np.zeros((rows, cap), np.uint32),
-            "keep_probs": np.zeros((rows, cap), np.float32),
+            "keep_probs": np.zeros((rows, cap), np.float32), "norm": np.zeros(rows, np.float32),
         }
         ver = Verify(cap, *(res[k].ctypes.data for k in
-                            ("topk_count", "topk_ids", "keep_count", "keep_ids", "keep_probs")))
+                            ("topk_count", "topk_ids", "keep_count", "keep_ids", "keep_probs", "norm")))
     rc = lib().tco_sample(C.byref(params), logits.ctypes.data, rows, V,
                           None if ho is None else ho.ctypes.data,
                           None if hi is None else hi.ctypes.data,

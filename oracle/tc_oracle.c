@@ -289,15 +289,18 @@ void tco_qwen_top_p(float* row, size_t V, double p, uint32_t* flags) {
 }
 
 /* candle_nn::ops::softmax_last_dim on CPU (one row). */
-void tco_softmax_last_dim(float* row, size_t V) {
-  if (V == 0) return;
+static float softmax_last_dim_sum(float* row, size_t V) {
+  if (V == 0) return NAN;
   float max = row[0];
   for (size_t i = 1; i < V; i++) max = rmaxf(max, row[i]);
   for (size_t i = 0; i < V; i++) row[i] = expf(row[i] - max);
   float sum = 0.0f;
   for (size_t i = 0; i < V; i++) sum += row[i];
   for (size_t i = 0; i < V; i++) row[i] /= sum;
+  return sum;
 }
+
+void tco_softmax_last_dim(float* row, size_t V) { (void)softmax_last_dim_sum(row, V); }
 
 /* sampling.rs:319-328; -1 = None */
 int64_t tco_qwen_first_cdf_index(const float* row, size_t V, float thr) {
@@ -314,15 +317,19 @@ int64_t tco_qwen_first_cdf_index(const float* row, size_t V, float thr) {
 /* ------------------------------------------------------------------------ */
 
 /* :95-105 */
-void tco_idx_log_softmax(float* row, size_t V) {
+/* returns log_sum, NaN when the row max is not finite (row left as is) */
+static float idx_log_softmax_ls(float* row, size_t V) {
   float max = -INFINITY;
   for (size_t i = 0; i < V; i++) max = rmaxf(max, row[i]);
-  if (!isfinite(max)) return;
+  if (!isfinite(max)) return NAN;
   float sum = -0.0f;
   for (size_t i = 0; i < V; i++) sum += expf(row[i] - max);
   float log_sum = logf(sum);
   for (size_t i = 0; i < V; i++) row[i] = (row[i] - max) - log_sum;
+  return log_sum;
 }
+
+void tco_idx_log_softmax(float* row, size_t V) { (void)idx_log_softmax_ls(row, V); }
 
 /* :108-116 */
 static void idx_softmax_f64(const double* row, size_t V, double* out) {
@@ -568,6 +575,7 @@ typedef struct {
   uint32_t* keep;
   float* keep_p;
   uint32_t cap;
+  float norm;         /* indextts log_sum; qwen / cosyvoice3 softmax denominator */
 } row_verify;
 
 static void rv_set_topk_from_row(row_verify* rv, const float* row, size_t V) {
@@ -608,7 +616,8 @@ static int row_qwen(const tco_params* p, float* x, size_t V, const uint32_t* ids
   if (p->top_p < 1.0 && p->top_p > 0.0) tco_qwen_top_p(x, V, p->top_p, flags);
   unsigned char* alive = rv ? (unsigned char*)malloc(V) : NULL;
   if (rv) for (size_t i = 0; i < V; i++) alive[i] = x[i] != -INFINITY;
-  tco_softmax_last_dim(x, V);
+  float norm = softmax_last_dim_sum(x, V);
+  if (rv) rv->norm = norm;
   int64_t i = tco_qwen_first_cdf_index(x, V, u);
   *tok = i < 0 ? 0u : (uint32_t)i;
   if (rv) {
@@ -633,8 +642,10 @@ static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const u
     for (size_t i = 0; i < V; i++) x[i] = expf(x[i] - max);
     float sum = dev_order_sum(x, V, row, p);
     for (size_t i = 0; i < V; i++) x[i] /= sum;
+    if (rv) rv->norm = sum;
   } else {
-    tco_softmax_last_dim(x, V);
+    float sum = softmax_last_dim_sum(x, V);
+    if (rv) rv->norm = sum;
   }
   int used = 0;
   uint32_t nc = 0;
@@ -677,19 +688,10 @@ static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const u
 static int row_indextts(const tco_params* p, float* x, size_t V, size_t row, const uint32_t* ids,
                         size_t n_ids, double u, uint32_t* tok, uint32_t* flags, row_verify* rv) {
   (void)flags;
-  if (p->dev_threads > 0) {
-    float max = -INFINITY;
-    for (size_t i = 0; i < V; i++) max = rmaxf(max, x[i]);
-    if (isfinite(max)) {
-      float* e = (float*)malloc(V * sizeof(float));
-      for (size_t i = 0; i < V; i++) e[i] = (float)exp((double)(x[i] - max)); /* correctly rounded */
-      float sum = dev_order_sum(e, V, row, p);
-      float log_sum = (float)log((double)sum);
-      for (size_t i = 0; i < V; i++) x[i] = (x[i] - max) - log_sum;
-      free(e);
-    }
-  } else {
-    tco_idx_log_softmax(x, V);
+  (void)row;
+  {
+    float ls = idx_log_softmax_ls(x, V);
+    if (rv) rv->norm = ls;
   }
   if (p->penalty != 1.0) tco_idx_penalty(x, V, ids, n_ids, p->penalty);
   if (p->typical) tco_idx_typical(x, V, p->typical_mass, 2);
@@ -889,6 +891,7 @@ static void sample_one_row(const tco_params* p, const float* logits, size_t r, s
     rv->keep = ver->keep_ids ? ver->keep_ids + r * ver->cap : (uint32_t*)calloc(ver->cap, 4);
     rv->keep_p = ver->keep_probs ? ver->keep_probs + r * ver->cap : (float*)calloc(ver->cap, 4);
     rv->n_topk = rv->n_keep = 0;
+    rv->norm = NAN;
   }
   uint32_t tok = 0, flags = 0;
   int st;
@@ -911,6 +914,7 @@ static void sample_one_row(const tco_params* p, const float* logits, size_t r, s
   if (rv) {
     if (ver->topk_count) ver->topk_count[r] = rv->n_topk;
     if (ver->keep_count) ver->keep_count[r] = rv->n_keep;
+    if (ver->norm) ver->norm[r] = rv->norm;
     if (!ver->topk_ids) free(rv->topk);
     if (!ver->keep_ids) free(rv->keep);
     if (!ver->keep_probs) free(rv->keep_p);

@@ -91,6 +91,8 @@ typedef struct tco_verify {
   uint32_t* keep_count;    /* [rows] size of the final candidate set */
   uint32_t* keep_ids;      /* [rows*cap] ascending vocab ids */
   float* keep_probs;       /* [rows*cap] probability used by the draw, per kept id */
+  float* norm;             /* [rows] indextts log_sum, qwen / cosyvoice3 softmax denominator
+                              (NaN where the row has none) */
 } tco_verify;
 
 /* ---- RNGs (integer-exact restatements) ---- */

@@ -57,6 +57,7 @@ class VerifyOut(C.Structure):
         ("d_keep_count", C.c_void_p),
         ("d_keep_ids", C.c_void_p),
         ("d_keep_probs", C.c_void_p),
+        ("d_norm", C.c_void_p),
     ]
 
 

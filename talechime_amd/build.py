@@ -4,8 +4,8 @@
 
 Steps:
   1. compile and run csrc/gen_expf_table.c (host, gcc) to produce
-     csrc/_gen/expf_glibc_exc.inc -- skipped when the include is newer than the
-     generator and tc_math.h;
+     csrc/_gen/expf_glibc_exc.inc and csrc/_gen/logf_glibc_exc.inc -- skipped
+     when both includes are newer than the generator and tc_math.h;
   2. hipcc --offload-arch=gfx950 -shared the kernels and the C ABI into
      talechime_amd/libtalechime_hip.so.
 
@@ -52,16 +52,17 @@ def _newer(target: str, *deps: str) -> bool:
 def gen_tables(force: bool = False) -> None:
     os.makedirs(GEN, exist_ok=True)
     inc = os.path.join(GEN, "expf_glibc_exc.inc")
+    linc = os.path.join(GEN, "logf_glibc_exc.inc")
     src = os.path.join(CSRC, "gen_expf_table.c")
     hdr = os.path.join(CSRC, "tc_math.h")
-    if not force and _newer(inc, src, hdr):
+    if not force and _newer(inc, src, hdr) and _newer(linc, src, hdr):
         return
     exe = os.path.join(GEN, "gen_expf_table")
     subprocess.run(["gcc", "-O2", "-fopenmp", "-fno-fast-math", "-ffp-contract=off", "-o", exe, src, "-lm"],
                    check=True)
-    tmp = inc + ".tmp"
-    subprocess.run([exe, tmp], check=True)
-    os.replace(tmp, inc)
+    subprocess.run([exe, inc + ".tmp", linc + ".tmp"], check=True)
+    os.replace(inc + ".tmp", inc)
+    os.replace(linc + ".tmp", linc)
 
 
 def hipcc() -> str:

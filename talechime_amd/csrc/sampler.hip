@@ -27,10 +27,18 @@
 
 #include "../../include/talechime_hip.h"
 #include "tc_device.h"
+#include "tc_select.h"
+#include "tc_seqsum.h"
 
 namespace tc {
 
 constexpr int kSurvCap = 1024;      // survivors held in LDS per row
+
+// Register-resident row shapes: ITEMS elements per thread, at most
+// max_threads(ITEMS) threads (which sets the register budget per thread).
+constexpr int max_threads(int items) { return items == 8 ? 1024 : (items == 16 ? 768 : 704); }
+
+
 constexpr int kMaxVocabReg = 16384; // register-resident rows: V + alignment <= 1024 * 16
 
 struct RowArgs {
@@ -53,6 +61,7 @@ struct RowArgs {
   uint32_t* keep_count;
   uint32_t* keep_ids;
   float* keep_probs;
+  float* norm;  // optional [rows] normaliser output
   // parameters, prepared on the host
   int do_pen;
   float pen_f;    // penalty as f32
@@ -98,7 +107,7 @@ __device__ __forceinline__ void hist_range(const RowArgs& a, int row, uint32_t* 
 
 // Byte map of the ids in the row's history (ids >= V ignored).  Returns true if
 // some id was >= V.
-__device__ bool build_seen(const RowArgs& a, int row, uint8_t* seen, BlockScratch& s) {
+__device__ __forceinline__ bool build_seen(const RowArgs& a, int row, uint8_t* seen, BlockScratch& s) {
   const int V = a.V;
   uint32_t* w = reinterpret_cast<uint32_t*>(seen);
   for (int i = threadIdx.x; i < (V + 3) / 4; i += blockDim.x) w[i] = 0u;
@@ -118,7 +127,7 @@ __device__ bool build_seen(const RowArgs& a, int row, uint8_t* seen, BlockScratc
 // Ordered compaction of the selected elements into LDS (vocabulary order).
 // Returns the number selected (may exceed kSurvCap; then only the count is valid).
 template <int ITEMS>
-__device__ uint32_t compact(const float (&x)[ITEMS], uint32_t sel, int e0, SurvLds& sv, BlockScratch& s) {
+__device__ __forceinline__ uint32_t compact(const float (&x)[ITEMS], uint32_t sel, int e0, SurvLds& sv, BlockScratch& s) {
   uint32_t c = __builtin_popcount(sel);
   uint32_t total;
   uint32_t pos = block_excl_scan(c, s, &total);
@@ -135,7 +144,7 @@ __device__ uint32_t compact(const float (&x)[ITEMS], uint32_t sel, int e0, SurvL
   return total;
 }
 
-__device__ void write_topk(const RowArgs& a, int row, const SurvLds& sv, uint32_t n) {
+__device__ __forceinline__ void write_topk(const RowArgs& a, int row, const SurvLds& sv, uint32_t n) {
   if (a.topk_count == nullptr) return;
   if (threadIdx.x == 0) a.topk_count[row] = n;
   if (n > (uint32_t)kSurvCap) return;  // only the count is known
@@ -145,7 +154,7 @@ __device__ void write_topk(const RowArgs& a, int row, const SurvLds& sv, uint32_
 
 // Rank-order sort of the n survivors: keys built by the caller in sv.key[0..n),
 // padded to a power of two.
-__device__ void sort_survivors(SurvLds& sv, uint32_t n) {
+__device__ __forceinline__ void sort_survivors(SurvLds& sv, uint32_t n) {
   int n_pad = next_pow2((int)n < 2 ? 2 : (int)n);
   for (int j = (int)n + threadIdx.x; j < n_pad; j += blockDim.x) sv.key[j] = ~0ull;
   __syncthreads();
@@ -160,7 +169,12 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int row, uint32_t t
   }
 }
 
+__device__ __forceinline__ void put_norm(const RowArgs& a, int row, float v) {
+  if (a.norm && threadIdx.x == 0) a.norm[row] = v;
+}
+
 __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
+  if (threadIdx.x == 0 && a.norm) a.norm[row] = __builtin_nanf("");
   if (threadIdx.x == 0) {
     if (a.topk_count) a.topk_count[row] = 0;
     if (a.keep_count) a.keep_count[row] = 0;
@@ -169,7 +183,7 @@ __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
 
 // ================================================================ qwen
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_qwen(RowArgs a) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
   __shared__ uint8_t s_seen[kMaxVocabReg];
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
@@ -262,11 +276,13 @@ __global__ void __launch_bounds__(kMaxThreads) k_qwen(RowArgs a) {
   if (n > (uint32_t)kSurvCap) {
     finish_row(a, row, 0u, TC_EUNSUPPORTED, flags);
     if (t == 0 && a.keep_count) a.keep_count[row] = 0;
+    put_norm(a, row, __builtin_nanf(""));
     return;
   }
   if (n == 0) {  // every entry -inf (or NaN): the reference's CDF is NaN -> index 0
     finish_row(a, row, 0u, TC_OK, flags);
     if (t == 0 && a.keep_count) a.keep_count[row] = 0;
+    put_norm(a, row, __builtin_nanf(""));
     return;
   }
   // softmax numerators over the survivors; the row max is the largest survivor
@@ -318,6 +334,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_qwen(RowArgs a) {
     if (a.out_status) a.out_status[row] = TC_OK;
     if (a.out_flags) a.out_flags[row] = flags;
     s_out[2] = __float_as_uint(S2);
+    if (a.norm) a.norm[row] = S2;
   }
   if (a.keep_count) {
     __syncthreads();
@@ -338,12 +355,243 @@ __global__ void __launch_bounds__(kMaxThreads) k_qwen(RowArgs a) {
 }
 
 // ================================================================ indextts
+// log_softmax (generation.rs:95-105) with the reference's sequential f32
+// denominator reproduced exactly; returns log_sum, or NaN when a NaN logit
+// makes the sum NaN.  Leaves x untouched when the row max is not finite.
+template <int ITEMS>
+__device__ __forceinline__ float exact_log_softmax(float (&x)[ITEMS], uint32_t vm, int e0, SeqLds& sq, ScanLds& sc,
+                                                   BlockScratch& s, float* stage, int V) {
+  float m = -__builtin_inff();
+  uint32_t nan_any = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((vm >> i) & 1u) {
+      m = rmaxf(m, x[i]);
+      nan_any |= __builtin_isnan(x[i]) ? 1u : 0u;
+    }
+  const float mx = block_max(m, s);
+  nan_any = block_or_u(nan_any, s);
+  if (!__builtin_isfinite(mx)) return __builtin_nanf("");
+  float S;
+  if (nan_any) {
+    S = __builtin_nanf("");
+  } else {
+    // terms exp(x - max): approximate (tc_expf_fast) where that is safe to
+    // test against; the sum computes the exact glibc bits where it needs them
+    float ap[ITEMS];
+    uint32_t exm = 0, slow = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const float d = x[i] - mx;
+      const bool v = (vm >> i) & 1u;
+      ap[i] = (v && d >= -87.0f) ? tc_expf_fast(d) : 0.0f;
+      if (!v) exm |= 1u << i;
+      if (v && !(d >= -87.0f)) slow |= 1u << i;
+    }
+    auto exact = [mx](float xi) { return expf_glibc(xi - mx); };
+    while (__ballot(slow != 0u)) {  // tiny terms: the exact value up front
+      if (slow) {
+        const int i = __builtin_ctz(slow);
+        put_item<ITEMS>(ap, i, exact(pick_item<ITEMS>(x, i)));
+        exm |= 1u << i;
+        slow &= slow - 1u;
+      }
+    }
+    SeqThread<ITEMS> th;
+    if (!block_seqsum<ITEMS>(ap, exm, x, exact, e0, TC_EXPF_FAST_ULPS, th, sq, sc, &S)) {
+      float ex[ITEMS];
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) ex[i] = ((vm >> i) & 1u) ? expf_glibc(x[i] - mx) : 0.0f;
+      S = block_seqsum_slow<ITEMS>(ex, e0, V, stage, kMaxVocabReg / 4, &sq.S);
+    }
+  }
+  const float L = logf_glibc(S);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) x[i] = (x[i] - mx) - L;
+  return L;
+}
+
+// Candidates held by one wave, two per lane (candidate i in lane i % 64 of
+// slot i / 64), with their rank under (key descending, index descending):
+// rank = number of candidates that beat it.  Counting costs one broadcast per
+// candidate and no shuffles.
+struct WaveCands {
+  uint32_t n;        // candidates (uniform)
+  uint32_t key[2];
+  uint32_t pos[2];   // vocabulary id
+  uint32_t rank[2];
+  bool has[2];
+};
+
+__device__ __forceinline__ void load_wave_cands(const SelLds& sl, uint32_t n_in, WaveCands& c) {
+  const int lane = lane_id();
+  c.n = (uint32_t)__builtin_amdgcn_readfirstlane((int)n_in);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t i = (uint32_t)(q * kWave + lane);
+    c.has[q] = i < c.n;
+    const uint64_t v = c.has[q] ? candidate_at(sl, i) : 0ull;
+    c.pos[q] = (uint32_t)v;
+    c.key[q] = (uint32_t)(v >> 32);
+    c.rank[q] = 0;
+  }
+  for (uint32_t j = 0; j < c.n; ++j) {
+    const uint32_t kj = readlane_u32(j < 64 ? c.key[0] : c.key[1], j & 63);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t i = (uint32_t)(q * kWave + lane);
+      c.rank[q] += (kj > c.key[q] || (kj == c.key[q] && j > i)) ? 1u : 0u;
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (!c.has[q]) c.rank[q] = 0xffffffffu;
+}
+
+// Candidate index (uniform) holding rank r.
+__device__ __forceinline__ uint32_t cand_of_rank(const WaveCands& c, uint32_t r) {
+  const uint64_t b0 = __ballot(c.rank[0] == r), b1 = __ballot(c.rank[1] == r);
+  return b0 ? (uint32_t)__builtin_ctzll(b0) : 64u + (uint32_t)__builtin_ctzll(b1);
+}
+
+__device__ __forceinline__ double pick_d(const double (&v)[2], uint32_t i) {
+  return readlane_f64(i < 64 ? v[0] : v[1], i & 63);
+}
+
+// One-wave finish of an indextts row over its n <= SelLds::kCapF top-k
+// candidates (vocabulary order in the wave regions): top-k cut, top-p
+// (generation.rs:169-194), then one draw of sample_without_replacement
+// (generation.rs:280-303).  All scores are finite here.
+__device__ __forceinline__ void indextts_finish(const RowArgs& a, int row, const SelLds& sl, uint32_t n_in) {
+  const int lane = lane_id();
+  WaveCands c;
+  load_wave_cands(sl, n_in, c);
+  float sc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) sc[q] = untkey(c.key[q]);
+  const uint32_t K = (uint32_t)a.K;
+  const uint32_t ik = cand_of_rank(c, K - 1);
+  const float kth = untkey(readlane_u32(ik < 64 ? c.key[0] : c.key[1], ik & 63));
+  bool surv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) surv[q] = c.has[q] && !(sc[q] < kth);
+  const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
+  const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  uint64_t rm0 = 0, rm1 = 0;
+  if (a.do_topp) {
+    // f64 softmax over the row: removed entries are -inf and add exact zeros
+    const uint32_t i0 = cand_of_rank(c, 0);
+    const double mxd = (double)readlane_f32(i0 < 64 ? sc[0] : sc[1], i0 & 63);
+    double w[2], p[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
+    double sum = -0.0;
+    for (uint64_t m = sm0; m; m &= m - 1) sum += readlane_f64(w[0], __builtin_ctzll(m));
+    for (uint64_t m = sm1; m; m &= m - 1) sum += readlane_f64(w[1], __builtin_ctzll(m));
+#pragma unroll
+    for (int q = 0; q < 2; ++q) p[q] = w[q] / sum;
+    // ascending stable order = ranks from the last survivor back to 0
+    double cum = 0.0;
+    const double lim = 1.0 - a.top_p_d;
+    for (int r = (int)ns - 1; r >= 0; --r) {
+      const uint32_t i = cand_of_rank(c, (uint32_t)r);
+      cum += pick_d(p, i);
+      if (cum <= lim) {
+        if (i < 64) rm0 |= 1ull << i;
+        else rm1 |= 1ull << (i - 64);
+      }
+    }
+    for (uint32_t r = 0; r < ns && r < (uint32_t)a.min_keep; ++r) {
+      const uint32_t i = cand_of_rank(c, r);
+      if (i < 64) rm0 &= ~(1ull << i);
+      else rm1 &= ~(1ull << (i - 64));
+    }
+  }
+  const uint64_t lm0 = sm0 & ~rm0, lm1 = sm1 & ~rm1;
+  bool live[2];
+  live[0] = (lm0 >> lane) & 1ull;
+  live[1] = (lm1 >> lane) & 1ull;
+  const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
+  // the draw: softmax over the live entries in vocabulary order
+  double ml = -__builtin_inf();
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (live[q]) ml = rmaxd(ml, (double)sc[q] + 0.0);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ml = rmaxd(ml, __shfl_xor(ml, o));
+  double ev[2], wv[2], acc[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    ev[q] = live[q] ? tc_exp_d(((double)sc[q] + 0.0) - ml) : 0.0;
+    acc[q] = 0.0;
+  }
+  double sum2 = -0.0;
+  for (uint64_t m = lm0; m; m &= m - 1) sum2 += readlane_f64(ev[0], __builtin_ctzll(m));
+  for (uint64_t m = lm1; m; m &= m - 1) sum2 += readlane_f64(ev[1], __builtin_ctzll(m));
+#pragma unroll
+  for (int q = 0; q < 2; ++q) wv[q] = live[q] ? ev[q] / sum2 : 0.0;
+  // inverse_cdf: the running sum is also `total` (zero weights add nothing)
+  double run = 0.0;
+  for (uint64_t m = lm0; m; m &= m - 1) {
+    const int l = __builtin_ctzll(m);
+    run += readlane_f64(wv[0], l);
+    if (lane == l) acc[0] = run;
+  }
+  for (uint64_t m = lm1; m; m &= m - 1) {
+    const int l = __builtin_ctzll(m);
+    run += readlane_f64(wv[1], l);
+    if (lane == l) acc[1] = run;
+  }
+  const double uu = reinterpret_cast<const double*>(a.uniforms)[row] * run;
+  const uint64_t hit0 = __ballot(live[0] && wv[0] > 0.0 && acc[0] > uu);
+  const uint64_t hit1 = __ballot(live[1] && wv[1] > 0.0 && acc[1] > uu);
+  const uint64_t pz0 = __ballot(live[0] && wv[0] > 0.0), pz1 = __ballot(live[1] && wv[1] > 0.0);
+  uint32_t pick;
+  if (hit0) pick = (uint32_t)__builtin_ctzll(hit0);
+  else if (hit1) pick = 64 + (uint32_t)__builtin_ctzll(hit1);
+  else if (pz1) pick = 64 + 63 - (uint32_t)__builtin_clzll(pz1);
+  else if (pz0) pick = 63 - (uint32_t)__builtin_clzll(pz0);
+  else pick = lm0 ? (uint32_t)__builtin_ctzll(lm0) : 64 + (uint32_t)__builtin_ctzll(lm1);
+  const uint32_t tok = nl ? readlane_u32(pick < 64 ? c.pos[0] : c.pos[1], pick & 63) : 0u;
+  if (lane == 0) {
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = nl ? TC_OK : TC_ETOOFEW;
+    if (a.out_flags) a.out_flags[row] = 0u;
+    if (a.topk_count) {
+      a.topk_count[row] = ns;
+      a.keep_count[row] = nl;
+    }
+  }
+  if (a.topk_count) {
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint64_t smq = q == 0 ? sm0 : sm1, lmq = q == 0 ? lm0 : lm1;
+      const uint32_t so = q == 0 ? 0u : (uint32_t)__popcll(sm0), lo = q == 0 ? 0u : (uint32_t)__popcll(lm0);
+      if (surv[q]) {
+        const uint32_t j = so + (uint32_t)__popcll(smq & below);
+        if (j < a.cap) a.topk_ids[(size_t)row * a.cap + j] = c.pos[q];
+      }
+      if (live[q]) {
+        const uint32_t j = lo + (uint32_t)__popcll(lmq & below);
+        if (j < a.cap) {
+          a.keep_ids[(size_t)row * a.cap + j] = c.pos[q];
+          a.keep_probs[(size_t)row * a.cap + j] = (float)wv[q];
+        }
+      }
+    }
+  }
+}
+
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_indextts(RowArgs a) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
   __shared__ uint8_t s_seen[kMaxVocabReg];
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
   __shared__ BlockScratch s;
+  __shared__ ScanLds sc;
+  __shared__ SeqLds sq;
+  __shared__ SelLds sl;
   __shared__ uint32_t s_out[4];
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
@@ -353,23 +601,8 @@ __global__ void __launch_bounds__(kMaxThreads) k_indextts(RowArgs a) {
   const uint32_t vm = valid_mask<ITEMS>(V, shift);
   const int e0 = t * ITEMS - shift;
   if (a.do_pen) build_seen(a, row, s_seen, s);
-
-  // log_softmax (generation.rs:95-105)
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i)
-    if ((vm >> i) & 1u) m = rmaxf(m, x[i]);
-  const float mx = block_max(m, s);
-  if (__builtin_isfinite(mx)) {
-    float part = 0.0f;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-      if ((vm >> i) & 1u) part += tc_expf_cr(x[i] - mx);
-    const float S = block_sum(part, s);
-    const float L = tc_logf_cr(S);
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) x[i] = (x[i] - mx) - L;
-  }
+  const float log_sum = exact_log_softmax<ITEMS>(x, vm, e0, sq, sc, s, reinterpret_cast<float*>(&sv), V);
+  put_norm(a, row, log_sum);
   // repetition penalty on the log-probs (generation.rs:122-134), temperature (137-142)
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
@@ -379,7 +612,32 @@ __global__ void __launch_bounds__(kMaxThreads) k_indextts(RowArgs a) {
     if (a.do_temp) v = v / a.t_f;
     x[i] = v;
   }
-  // top-k (generation.rs:148-161): drop scores strictly below the k-th largest (total order)
+  // fast path: top-k of at most 64 with every score finite -> candidates from
+  // the per-thread-maximum bound, finished by one wave
+  if (a.K > 0 && a.K <= 64 && a.K < V) {
+    uint32_t key[ITEMS];
+    uint32_t nf = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const bool v = (vm >> i) & 1u;
+      key[i] = v ? tkey(x[i]) : 0u;
+      nf |= (v && !__builtin_isfinite(x[i])) ? 1u : 0u;
+    }
+    uint32_t T0 = block_topk_bound<ITEMS>(key, vm, a.K, sl);
+    if (T0 == 0x80000000u) T0 = 0x7fffffffu;  // -0.0 compares equal to a +0.0 cut
+    uint32_t sel = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if (((vm >> i) & 1u) && key[i] >= T0) sel |= 1u << i;
+    bool of;
+    uint32_t nfl;
+    const uint32_t n = block_compact_candidates<ITEMS>(key, sel, e0, sl, nf != 0u, &of, &nfl);
+    if (!of && !nfl && n <= (uint32_t)SelLds::kCapF) {
+      if (wave_id() == 0) indextts_finish(a, row, sl, n);
+      return;
+    }
+  }
+  // general path: radix select over the whole row, survivors staged in LDS
   float kth = -__builtin_inff();
   bool cut = false;
   if (a.K > 0 && a.K < V) {
@@ -497,7 +755,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_indextts(RowArgs a) {
 
 // ================================================================ cosyvoice3
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_cosy(RowArgs a) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_cosy(RowArgs a) {
   __shared__ uint8_t s_seen[kMaxVocabReg];  // staging for the fallback CDF
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
@@ -527,6 +785,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_cosy(RowArgs a) {
     part += x[i];
   }
   const float S = block_sum(part, s);
+  put_norm(a, row, S);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = x[i] / S;  // probabilities
   // nucleus (llm.rs:556-592): rank by (prob desc, id asc); at most top_k candidates
@@ -648,7 +907,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_cosy(RowArgs a) {
 
 // ================================================================ moss
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_moss(RowArgs a) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_moss(RowArgs a) {
   __shared__ uint8_t s_seen[kMaxVocabReg];
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
@@ -658,6 +917,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_moss(RowArgs a) {
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
   float x[ITEMS];
   int shift;
+  put_norm(a, row, __builtin_nanf(""));
   load_row<ITEMS>(rp, V, x, &shift);
   const uint32_t vm = valid_mask<ITEMS>(V, shift);
   const int e0 = t * ITEMS - shift;
@@ -765,7 +1025,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_moss(RowArgs a) {
 
 // ================================================================ moss-nano
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_nano(RowArgs a) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_nano(RowArgs a) {
   __shared__ uint8_t s_seen[kMaxVocabReg];
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
@@ -775,6 +1035,7 @@ __global__ void __launch_bounds__(kMaxThreads) k_nano(RowArgs a) {
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
   float x[ITEMS];
   int shift;
+  put_norm(a, row, __builtin_nanf(""));
   load_row<ITEMS>(rp, V, x, &shift);
   const uint32_t vm = valid_mask<ITEMS>(V, shift);
   const int e0 = t * ITEMS - shift;
@@ -939,7 +1200,7 @@ __global__ void k_update_penalty_mask(float* mask, int V, const uint32_t* token)
 }
 
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(kMaxThreads) k_greedy(const InT* logits, long long ld, int V, uint32_t* out) {
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_greedy(const InT* logits, long long ld, int V, uint32_t* out) {
   __shared__ uint64_t s_best[kMaxWaves];
   __shared__ uint32_t s_nan0;
   const int row = blockIdx.x, t = threadIdx.x;
@@ -1018,11 +1279,11 @@ struct DeviceGuard {
 // multiple of 64 in [256, 1024].
 bool pick_shape(int V, int dtype, int* items, int* threads) {
   const int pad = dtype == TC_BF16 ? 7 : 3;
-  for (int it : {8, 16}) {
+  for (int it : {8, 16, 24}) {
     int nt = (V + pad + it - 1) / it;
     nt = (nt + 63) / 64 * 64;
     if (nt < 256) nt = 256;
-    if (nt <= tc::kMaxThreads) {
+    if (nt <= tc::max_threads(it)) {
       *items = it;
       *threads = nt;
       return true;
@@ -1037,10 +1298,12 @@ bool pick_shape(int V, int dtype, int* items, int* threads) {
     dim3 g(rows), b(threads);                                                                    \
     if (dtype == TC_F32) {                                                                       \
       if (items == 8) hipLaunchKernelGGL((tc::NAME<float, 8>), g, b, 0, st, a);                  \
-      else hipLaunchKernelGGL((tc::NAME<float, 16>), g, b, 0, st, a);                            \
+      else if (items == 16) hipLaunchKernelGGL((tc::NAME<float, 16>), g, b, 0, st, a);           \
+      else hipLaunchKernelGGL((tc::NAME<float, 24>), g, b, 0, st, a);                            \
     } else {                                                                                     \
       if (items == 8) hipLaunchKernelGGL((tc::NAME<uint16_t, 8>), g, b, 0, st, a);               \
-      else hipLaunchKernelGGL((tc::NAME<uint16_t, 16>), g, b, 0, st, a);                         \
+      else if (items == 16) hipLaunchKernelGGL((tc::NAME<uint16_t, 16>), g, b, 0, st, a);        \
+      else hipLaunchKernelGGL((tc::NAME<uint16_t, 24>), g, b, 0, st, a);                         \
     }                                                                                            \
     return hipGetLastError();                                                                    \
   }
@@ -1121,6 +1384,7 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
     a.keep_count = verify->d_keep_count;
     a.keep_ids = verify->d_keep_ids;
     a.keep_probs = verify->d_keep_probs;
+    a.norm = verify->d_norm;
   }
   a.eos_id = p->eos_id;
   a.exclude_id = p->exclude_id;
@@ -1305,10 +1569,12 @@ int tc_greedy_sample(const void* d_logits, int dtype, size_t rows, size_t vocab,
   dim3 g((unsigned)rows), b(threads);
   if (dtype == TC_F32) {
     if (items == 8) hipLaunchKernelGGL((tc::k_greedy<float, 8>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
-    else hipLaunchKernelGGL((tc::k_greedy<float, 16>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else if (items == 16) hipLaunchKernelGGL((tc::k_greedy<float, 16>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else hipLaunchKernelGGL((tc::k_greedy<float, 24>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
   } else {
     if (items == 8) hipLaunchKernelGGL((tc::k_greedy<uint16_t, 8>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
-    else hipLaunchKernelGGL((tc::k_greedy<uint16_t, 16>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else if (items == 16) hipLaunchKernelGGL((tc::k_greedy<uint16_t, 16>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else hipLaunchKernelGGL((tc::k_greedy<uint16_t, 24>), g, b, 0, st, (const uint16_t*)d_logits, (long long)ld, (int)vocab, d_out_ids);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TC_OK : hip_fail(e, "tc_greedy_sample");

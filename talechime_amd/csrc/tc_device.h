@@ -6,6 +6,7 @@
 
 #include "tc_math.h"
 #include "_gen/expf_glibc_exc.inc"
+#include "_gen/logf_glibc_exc.inc"
 
 namespace tc {
 
@@ -39,7 +40,7 @@ __device__ __forceinline__ double rmaxd(double a, double b) {
 // glibc's expf differs from the correctly rounded value only on the inputs in
 // tc_expf_exc_keys, all of which sit within TC_EXPF_BAND ulp of a rounding
 // midpoint; there it returns the neighbour on the far side of the midpoint.
-__device__ __noinline__ bool expf_is_exception(uint32_t b) {
+__device__ __forceinline__ bool expf_is_exception(uint32_t b) {
   uint32_t h = b >> 16;
   uint32_t lo = tc_expf_exc_index[h], hi = tc_expf_exc_index[h + 1];
   while (lo < hi) {
@@ -61,6 +62,37 @@ __device__ __forceinline__ float expf_glibc(float x) {
   if (tc_mid_dist(y, r) < TC_EXPF_BAND) {
     if (expf_is_exception(f2u(x))) r = u2f(tc_toward(y, r));
   }
+  return r;
+}
+
+// ---------------------------------------------------------------- glibc logf
+// glibc's logf on [1, 2^24) differs from tc_logf_cr only on the inputs in
+// tc_logf_exc_keys, all within TC_LOGF_BAND ulp of a rounding midpoint, where
+// it returns the neighbour across the midpoint.  Keys are bucketed by
+// (bits - bits(1.0f)) >> TC_LOGF_BUCKET_SHIFT.
+__device__ __forceinline__ bool logf_is_exception(uint32_t b) {
+  const uint32_t off = b - 0x3f800000u;
+  const uint32_t bk = off >> TC_LOGF_BUCKET_SHIFT;
+  if (bk >= TC_LOGF_NBUCKETS) return false;
+  uint32_t lo = tc_logf_exc_index[bk], hi = tc_logf_exc_index[bk + 1];
+  while (lo < hi) {
+    uint32_t mid = (lo + hi) >> 1;
+    uint32_t k = tc_logf_exc_keys[mid];
+    if (k == b) return true;
+    if (k < b) lo = mid + 1;
+    else hi = mid;
+  }
+  return false;
+}
+
+// Rust's f32::ln (glibc logf) for x in [1, 2^24); other inputs get the
+// correctly rounded value.
+__device__ __forceinline__ float logf_glibc(float x) {
+  if (!(x >= 1.0f && x < 16777216.0f)) return tc_logf_cr(x);
+  if (x == 1.0f) return 0.0f;
+  double y = tc_log_d((double)x);
+  float r = (float)y;
+  if (tc_mid_dist(y, r) < TC_LOGF_BAND && logf_is_exception(f2u(x))) r = u2f(tc_toward(y, r));
   return r;
 }
 
@@ -106,7 +138,7 @@ struct BlockScratch {
 };
 
 // Max over the block (NaN ignored); every thread gets the result.
-__device__ float block_max(float v, BlockScratch& s) {
+__device__ __forceinline__ float block_max(float v, BlockScratch& s) {
   v = wave_max(v);
   if (lane_id() == 0) s.f[wave_id()] = v;
   __syncthreads();
@@ -118,7 +150,7 @@ __device__ float block_max(float v, BlockScratch& s) {
 
 // Sum over the block: in-thread order, then a butterfly inside each wave, then
 // the wave sums in wave order.  Deterministic for a fixed block shape.
-__device__ float block_sum(float v, BlockScratch& s) {
+__device__ __forceinline__ float block_sum(float v, BlockScratch& s) {
   v = wave_sum(v);
   if (lane_id() == 0) s.f[wave_id()] = v;
   __syncthreads();
@@ -128,7 +160,7 @@ __device__ float block_sum(float v, BlockScratch& s) {
   return r;
 }
 
-__device__ double block_max_d(double v, BlockScratch& s) {
+__device__ __forceinline__ double block_max_d(double v, BlockScratch& s) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = rmaxd(v, __shfl_xor(v, o));
   if (lane_id() == 0) s.d[wave_id()] = v;
@@ -139,7 +171,7 @@ __device__ double block_max_d(double v, BlockScratch& s) {
   return r;
 }
 
-__device__ uint32_t block_sum_u(uint32_t v, BlockScratch& s) {
+__device__ __forceinline__ uint32_t block_sum_u(uint32_t v, BlockScratch& s) {
   v = wave_sum_u(v);
   if (lane_id() == 0) s.u[wave_id()] = v;
   __syncthreads();
@@ -149,7 +181,7 @@ __device__ uint32_t block_sum_u(uint32_t v, BlockScratch& s) {
   return r;
 }
 
-__device__ uint32_t block_or_u(uint32_t v, BlockScratch& s) {
+__device__ __forceinline__ uint32_t block_or_u(uint32_t v, BlockScratch& s) {
   v = wave_or_u(v);
   if (lane_id() == 0) s.u[wave_id()] = v;
   __syncthreads();
@@ -160,7 +192,7 @@ __device__ uint32_t block_or_u(uint32_t v, BlockScratch& s) {
 }
 
 // Exclusive prefix sum over threads in thread order; *total gets the sum.
-__device__ uint32_t block_excl_scan(uint32_t v, BlockScratch& s, uint32_t* total) {
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, BlockScratch& s, uint32_t* total) {
   uint32_t inc = wave_incl_scan(v);
   if (lane_id() == kWave - 1) s.u[wave_id()] = inc;
   __syncthreads();
@@ -179,7 +211,7 @@ __device__ uint32_t block_excl_scan(uint32_t v, BlockScratch& s, uint32_t* total
 // Four MSB-first 8-bit radix passes with LDS histograms.  Returns false when
 // fewer than K keys are selected.
 template <int ITEMS>
-__device__ bool block_kth_largest(const uint32_t (&key)[ITEMS], uint32_t sel, uint32_t K,
+__device__ __forceinline__ bool block_kth_largest(const uint32_t (&key)[ITEMS], uint32_t sel, uint32_t K,
                                   uint32_t* hist /*[256]*/, BlockScratch& s, uint32_t* out) {
   uint32_t prefix = 0, pmask = 0;
   const int t = threadIdx.x;
@@ -224,7 +256,7 @@ __device__ bool block_kth_largest(const uint32_t (&key)[ITEMS], uint32_t sel, ui
 }
 
 // In-place ascending bitonic sort of n_pad (a power of two) 64-bit keys in LDS.
-__device__ void block_bitonic_sort(uint64_t* a, int n_pad) {
+__device__ __forceinline__ void block_bitonic_sort(uint64_t* a, int n_pad) {
   for (int k = 2; k <= n_pad; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
       for (int i = threadIdx.x; i < n_pad; i += blockDim.x) {
@@ -247,6 +279,155 @@ __device__ __forceinline__ int next_pow2(int n) {
   int p = 1;
   while (p < n) p <<= 1;
   return p;
+}
+
+// ---------------------------------------------------------------- wave sorts
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+// __builtin_amdgcn_readlane returns a signed int: go through uint32_t before
+// widening so the low word is not sign-extended.
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return ((uint64_t)readlane_u32((uint32_t)(v >> 32), l) << 32) | (uint64_t)readlane_u32((uint32_t)v, l);
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) { return u2f(__builtin_amdgcn_readlane(f2u(v), l)); }
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  return __longlong_as_double((long long)readlane_u64((uint64_t)__double_as_longlong(v), l));
+}
+
+// Bitonic sort of one key per lane into descending lane order.
+__device__ __forceinline__ uint32_t wave_sort_desc_u32(uint32_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      uint32_t o = __shfl_xor(v, j);
+      bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
+      v = take_max ? (o > v ? o : v) : (o < v ? o : v);
+    }
+  }
+  return v;
+}
+
+// Lane l holds element l of a bitonic sequence; returns it sorted descending.
+__device__ __forceinline__ uint32_t wave_bitonic_clean_desc_u32(uint32_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int j = kWave >> 1; j > 0; j >>= 1) {
+    uint32_t o = __shfl_xor(v, j);
+    v = ((lane & j) == 0) ? (o > v ? o : v) : (o < v ? o : v);
+  }
+  return v;
+}
+
+// Bitonic sort of 64*S 64-bit keys into descending order; element i lives in
+// lane i % 64 of slot i / 64.
+template <int S>
+__device__ __forceinline__ void wave_sort_desc_u64(uint64_t (&v)[S]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave * S; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= kWave) {
+        const int js = j / kWave;
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          if (sl & js) continue;
+          const int i = sl * kWave + lane;
+          const bool desc = (i & k) == 0;
+          uint64_t x = v[sl], y = v[sl + js];
+          uint64_t hi = x > y ? x : y, lo = x > y ? y : x;
+          v[sl] = desc ? hi : lo;
+          v[sl + js] = desc ? lo : hi;
+        }
+      } else {
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          const int i = sl * kWave + lane;
+          uint64_t o = shfl_xor_u64(v[sl], j);
+          bool take_max = ((i & j) == 0) == ((i & k) == 0);
+          v[sl] = take_max ? (o > v[sl] ? o : v[sl]) : (o < v[sl] ? o : v[sl]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- scans
+__device__ __forceinline__ double wave_incl_scan_d(double v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    double t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+__device__ __forceinline__ long long wave_incl_scan_ll(long long v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    long long t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive prefix over threads (thread order) of a double and of a
+// (count, int64) pair; *tot gets the totals.  One barrier each.
+struct ScanLds {
+  double d[kMaxWaves];
+  long long q[kMaxWaves];
+  uint32_t c[kMaxWaves];
+};
+
+__device__ __forceinline__ double block_excl_scan_d(double v, ScanLds& L, double* tot) {
+  double inc = wave_incl_scan_d(v);
+  if (lane_id() == kWave - 1) L.d[wave_id()] = inc;
+  __syncthreads();
+  double off = 0.0, all = 0.0;
+  for (int w = 0; w < num_waves(); ++w) {
+    double t = L.d[w];
+    if (w < wave_id()) off += t;
+    all += t;
+  }
+  __syncthreads();
+  *tot = all;
+  return off + (inc - v);
+}
+
+__device__ __forceinline__ void block_excl_scan_cq(uint32_t c, long long q, ScanLds& L, uint32_t* c_off, long long* q_off,
+                                   uint32_t* c_tot, long long* q_tot) {
+  uint32_t ci = wave_incl_scan(c);
+  long long qi = wave_incl_scan_ll(q);
+  if (lane_id() == kWave - 1) {
+    L.c[wave_id()] = ci;
+    L.q[wave_id()] = qi;
+  }
+  __syncthreads();
+  uint32_t co = 0, ca = 0;
+  long long qo = 0, qa = 0;
+  for (int w = 0; w < num_waves(); ++w) {
+    uint32_t tc = L.c[w];
+    long long tq = L.q[w];
+    if (w < wave_id()) {
+      co += tc;
+      qo += tq;
+    }
+    ca += tc;
+    qa += tq;
+  }
+  __syncthreads();
+  *c_off = co + ci - c;
+  *q_off = qo + qi - q;
+  *c_tot = ca;
+  *q_tot = qa;
 }
 
 // ---------------------------------------------------------------- row loads

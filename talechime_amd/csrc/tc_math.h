@@ -72,6 +72,28 @@ TC_HD float tc_expf_cr(float x) {
   return (float)tc_exp_d((double)x);
 }
 
+// exp(x) for x in [-87, 0] in float arithmetic only: k = rint(x / ln2),
+// r = x - k ln2 (Cody-Waite, ln2 split into a 16-bit head and a tail), the
+// degree-7 Taylor polynomial of exp(r) by Horner's rule with fmaf, scaled by
+// 2^k.  The table generator checks every input of [-87, 0] to be within
+// TC_EXPF_FAST_ULPS of tc_expf_cr.  The kernels use it for approximate terms
+// only; bits that can change a result are recomputed with tc_expf_cr.
+#define TC_EXPF_FAST_ULPS 1
+TC_HD float tc_expf_fast(float x) {
+  float kf = rintf(x * 1.44269504088896341f);
+  float r = fmaf(kf, -0.693145751953125f, x);
+  r = fmaf(kf, -1.42860682030941723212e-6f, r);
+  float p = 1.98412698412698412698e-4f;  // 1/7!
+  p = fmaf(p, r, 1.38888888888888888889e-3f);
+  p = fmaf(p, r, 8.33333333333333333333e-3f);
+  p = fmaf(p, r, 4.16666666666666666667e-2f);
+  p = fmaf(p, r, 1.66666666666666666667e-1f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  return ldexpf(p, (int)kf);
+}
+
 TC_HD double tc_log_d(double x) {
   // finite x > 0 only (callers handle 0, negatives, inf and NaN)
   const double ln2_hi = 6.93147180369123816490e-01;

@@ -57,6 +57,7 @@ class SampleResult:
     keep_count: torch.Tensor | None = None
     keep_ids: torch.Tensor | None = None
     keep_probs: torch.Tensor | None = None
+    norm: torch.Tensor | None = None
 
 
 class DeviceSampler:
@@ -122,8 +123,10 @@ class DeviceSampler:
             out.keep_count = torch.zeros(rows, dtype=torch.int32, device=dev)
             out.keep_ids = torch.zeros(rows, verify_cap, dtype=torch.int32, device=dev)
             out.keep_probs = torch.zeros(rows, verify_cap, dtype=torch.float32, device=dev)
+            out.norm = torch.zeros(rows, dtype=torch.float32, device=dev)
             ver = VerifyOut(verify_cap, out.topk_count.data_ptr(), out.topk_ids.data_ptr(),
-                            out.keep_count.data_ptr(), out.keep_ids.data_ptr(), out.keep_probs.data_ptr())
+                            out.keep_count.data_ptr(), out.keep_ids.data_ptr(), out.keep_probs.data_ptr(),
+                            out.norm.data_ptr())
         st = (stream or torch.cuda.current_stream(dev)).cuda_stream
         rc = load().tc_sample(self._ctx, C.byref(params), logits.data_ptr(), dt, rows, V, logits.stride(0),
                               ho, hi, uniforms.data_ptr(), out.ids.data_ptr(), out.status.data_ptr(),
@@ -136,9 +139,9 @@ def launch_shape(vocab: int, dtype: int = F32) -> tuple[int, int]:
     """(items per thread, threads per block) the library uses for one row of
     ``vocab`` logits (mirrors pick_shape in csrc/sampler.hip)."""
     pad = 7 if dtype == BF16 else 3
-    for items in (8, 16):
+    for items, max_t in ((8, 1024), (16, 768), (24, 704)):
         nt = -(-(vocab + pad) // items)
         nt = max(256, -(-nt // 64) * 64)
-        if nt <= 1024:
+        if nt <= max_t:
             return items, nt
     raise ValueError(f"vocab {vocab} exceeds the register-resident kernel")

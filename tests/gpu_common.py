@@ -42,7 +42,7 @@ def run_gpu(sampler: DeviceSampler, w, b, cap=64, **over):
     r = sampler.sample(p, logits, ho, hi, un, verify_cap=cap)
     torch.cuda.synchronize()
     out = {k: getattr(r, k).cpu().numpy() for k in ("ids", "status", "flags", "topk_count", "topk_ids",
-                                                    "keep_count", "keep_ids", "keep_probs")}
+                                                    "keep_count", "keep_ids", "keep_probs", "norm")}
     out["ids"] = out["ids"].view(np.uint32)
     return out
 

@@ -37,4 +37,4 @@ def test_struct_layout_matches_header():
     # offsets of tc_sample_params as laid out by the C compiler for this header
     assert ctypes.sizeof(_lib.SampleParams) == 72
     assert _lib.SampleParams.d_add_mask.offset == 56
-    assert ctypes.sizeof(_lib.VerifyOut) == 48
+    assert ctypes.sizeof(_lib.VerifyOut) == 56

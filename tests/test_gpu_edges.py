@@ -64,10 +64,10 @@ def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=Fa
     r = sampler.sample(p, dl, dho, dhi, du, verify_cap=CAP)
     torch.cuda.synchronize()
     g = {k: getattr(r, k).cpu().numpy() for k in ("ids", "status", "flags", "topk_count", "topk_ids",
-                                                  "keep_count", "keep_ids", "keep_probs")}
+                                                  "keep_count", "keep_ids", "keep_probs", "norm")}
     g["ids"] = g["ids"].view(np.uint32)
     dord = None
-    if dev_order and variant in (O.COSY_RAS, O.INDEXTTS):
+    if dev_order and variant == O.COSY_RAS:
         items, threads = launch_shape(V, 1 if bf16 else 0)
         dord = (items, threads, 8 if bf16 else 4, ld)
     okw = dict(kw)
@@ -91,9 +91,10 @@ def same(g, o, rows=None, probs_exact=True):
             assert g[c][r] == o[c][r], (r, c, g[c][r], o[c][r])
             n = min(int(g[c][r]), CAP)
             assert np.array_equal(g[i][r, :n].astype(np.uint32), o[i][r, :n]), (r, i)
+        assert np.array_equal(g["norm"][r:r + 1], o["norm"][r:r + 1], equal_nan=True), (r, g["norm"][r], o["norm"][r])
         n = min(int(g["keep_count"][r]), CAP)
         if probs_exact:
-            assert np.array_equal(g["keep_probs"][r, :n], o["keep_probs"][r, :n]), r
+            assert np.array_equal(g["keep_probs"][r, :n], o["keep_probs"][r, :n], equal_nan=True), r
         else:
             np.testing.assert_allclose(g["keep_probs"][r, :n], o["keep_probs"][r, :n], rtol=1e-5)
 
@@ -335,3 +336,72 @@ def test_building_blocks(sampler):
     _lib.check(L.tc_greedy_sample(dx.data_ptr(), 0, rows, V, V, out.data_ptr(), st))
     torch.cuda.synchronize()
     assert out.cpu().numpy().tolist() == [O.argmax(r) for r in x]
+
+
+# ------------------------------------------------------------------ exact sequential sums
+def _glibc_expf():
+    import ctypes
+    libm = ctypes.CDLL("libm.so.6")
+    f = libm.expf
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_float]
+    return f
+
+
+def _x_with_exp(expf, t):
+    """A float x whose glibc expf is exactly t (searched around log t), or None."""
+    x0 = np.array([np.log(np.float64(t))], np.float32).view(np.int32)[0]
+    for d in range(-48, 49):
+        x = np.array([x0 + d], np.int32).view(np.float32)[0]
+        if expf(float(x)) == np.float32(t):
+            return np.float32(x)
+    return None
+
+
+def _tie_row(expf, V, e, n_ties, seed):
+    """Row whose running softmax sum is exactly 2^e after 2^e zero logits (terms of 1.0),
+    followed by terms that are odd multiples of half the grid of binade e: each of
+    those adds rounds to even, a parity only the exact sequential sum settles."""
+    g = np.random.default_rng(seed)
+    row = np.full(V, -40.0, np.float32)
+    ones = 2 ** e
+    row[:ones] = 0.0
+    half = 2.0 ** (e - 24)
+    p = ones
+    lo_m, hi_m = int(0.025 / half) + 1, int(0.45 / half)
+    tries = 0
+    while n_ties and p < V - 1 and tries < 20 * n_ties + 200:
+        tries += 1
+        m = int(g.integers(lo_m, hi_m))
+        t = (2 * m + 1) * half
+        x = _x_with_exp(expf, t)
+        if x is None:
+            continue
+        row[p] = x
+        p += int(g.integers(1, 5))
+        n_ties -= 1
+    return row
+
+
+def test_indextts_exact_sum_adversarial(sampler):
+    # the log-sum must be the reference's bit for bit: sequential f32 adds of
+    # glibc expf terms, then glibc logf
+    expf = _glibc_expf()
+    V = 4000
+    g_ = np.random.default_rng(31)
+    rows = [np.zeros(V, np.float32),                                   # S = V exactly
+            _tie_row(expf, V, 1, 6, 1), _tie_row(expf, V, 4, 12, 2), _tie_row(expf, V, 9, 40, 3),
+            np.linspace(-40.0, 0.0, V).astype(np.float32),             # sum sweeps many binades
+            np.r_[np.full(1500, -100.0, np.float32), np.zeros(V - 1500, np.float32)],  # subnormal terms first
+            np.r_[np.full(V - 3, -95.0, np.float32), np.float32([0.0, -1.0, -2.0])],
+            (g_.standard_normal(V) * 4).astype(np.float32)]
+    x = np.stack(rows)
+    u = g_.random(len(rows))
+    hist = [[] for _ in rows]
+    for k, p in ((30, 0.8), (2, 0.5), (50, 0.95)):
+        g, o = run(sampler, O.INDEXTTS, x, hist, u, temperature=0.8, top_k=k, top_p=p, penalty=1.0, min_keep=2)
+        assert np.array_equal(g["norm"].view(np.uint32), o["norm"].view(np.uint32)), (g["norm"], o["norm"])
+        # row 0 ties all 4000 scores: more survivors than the LDS-staged general
+        # path holds (it reports TC_EUNSUPPORTED); its log-sum is still checked
+        assert g["status"][0] == _lib.TC_EUNSUPPORTED
+        same(g, o, rows=range(1, len(rows)), probs_exact=False)
