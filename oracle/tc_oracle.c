@@ -586,13 +586,24 @@ static void rv_set_topk_from_row(row_verify* rv, const float* row, size_t V) {
   rv->n_topk = n;
 }
 
-static void sort_ids_with_probs(uint32_t* ids, float* pr, uint32_t n) {
-  for (uint32_t i = 1; i < n; i++) {
-    uint32_t a = ids[i]; float b = pr ? pr[i] : 0.0f;
-    uint32_t j = i;
-    while (j > 0 && ids[j - 1] > a) { ids[j] = ids[j - 1]; if (pr) pr[j] = pr[j - 1]; j--; }
-    ids[j] = a; if (pr) pr[j] = b;
+/* Reports a candidate set given in any order as the verify contract wants it:
+ * the first `cap` ids of the whole set in ascending order (with their
+ * probabilities when pr is given). */
+static void rv_put_set(uint32_t* dst, float* dst_p, uint32_t cap, const uint32_t* ids, const float* pr,
+                       size_t n) {
+  uint64_t* t = (uint64_t*)malloc((n ? n : 1) * sizeof(uint64_t));
+  for (size_t j = 0; j < n; j++) {
+    float q = pr ? pr[j] : 0.0f;
+    uint32_t qb;
+    memcpy(&qb, &q, 4);
+    t[j] = ((uint64_t)ids[j] << 32) | qb;
   }
+  qsort(t, n, sizeof(uint64_t), cmp_u64);
+  for (size_t j = 0; j < n && j < cap; j++) {
+    dst[j] = (uint32_t)(t[j] >> 32);
+    if (dst_p) dst_p[j] = u2f((uint32_t)t[j]);
+  }
+  free(t);
 }
 
 /* qwen: caller penalty chain (synthesis.rs:1228-1279) + sample_cpu (sampling.rs:169-219). */
@@ -672,10 +683,8 @@ static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const u
   }
   *tok = top;
   if (rv) {
-    uint32_t n = nc < rv->cap ? nc : rv->cap;
-    for (uint32_t j = 0; j < n; j++) { rv->topk[j] = ci[j]; rv->keep[j] = ci[j]; rv->keep_p[j] = cpp[j]; }
-    sort_ids_with_probs(rv->topk, NULL, n);
-    sort_ids_with_probs(rv->keep, rv->keep_p, n);
+    rv_put_set(rv->topk, NULL, rv->cap, ci, NULL, nc);
+    rv_put_set(rv->keep, rv->keep_p, rv->cap, ci, cpp, nc);
     rv->n_topk = nc;
     rv->n_keep = nc;
   }
@@ -776,14 +785,15 @@ static int row_moss(const tco_params* p, float* x, size_t V, const uint32_t* his
   }
   *tok = result;
   if (rv) {
-    uint32_t n = (uint32_t)(k < rv->cap ? k : rv->cap);
-    for (uint32_t j = 0; j < n; j++) rv->topk[j] = (uint32_t)ranked[j];
-    sort_ids_with_probs(rv->topk, NULL, n);
+    uint32_t* ids = (uint32_t*)malloc(k * sizeof(uint32_t));
+    float* pk = (float*)malloc(k * sizeof(float));
+    for (size_t j = 0; j < k; j++) { ids[j] = (uint32_t)ranked[j]; pk[j] = (float)(w[j] / s); }
+    rv_put_set(rv->topk, NULL, rv->cap, ids, NULL, k);
+    rv_put_set(rv->keep, rv->keep_p, rv->cap, ids, pk, keep);
     rv->n_topk = (uint32_t)k;
-    n = (uint32_t)(keep < rv->cap ? keep : rv->cap);
-    for (uint32_t j = 0; j < n; j++) { rv->keep[j] = (uint32_t)ranked[j]; rv->keep_p[j] = (float)(w[j] / s); }
-    sort_ids_with_probs(rv->keep, rv->keep_p, n);
     rv->n_keep = (uint32_t)keep;
+    free(ids);
+    free(pk);
   }
   free(w);
   free(ranked);

@@ -754,12 +754,17 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 }
 
 // ================================================================ cosyvoice3
+// The softmax denominator and the fallback CDF are the reference's sequential
+// f32 sums, reproduced bit for bit by block_seqsum; the nucleus candidates are
+// exactly the top_k largest under (probability descending, id ascending).
 template <typename InT, int ITEMS>
 __global__ void __launch_bounds__(max_threads(ITEMS)) k_cosy(RowArgs a) {
-  __shared__ uint8_t s_seen[kMaxVocabReg];  // staging for the fallback CDF
+  __shared__ float s_stage[kMaxVocabReg / 4];  // staging for the one-lane fallback walks
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
   __shared__ BlockScratch s;
+  __shared__ ScanLds sc;
+  __shared__ SeqLds sq;
   __shared__ uint32_t s_out[4];
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
@@ -768,7 +773,8 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_cosy(RowArgs a) {
   load_row<ITEMS>(rp, V, x, &shift);
   const uint32_t vm = valid_mask<ITEMS>(V, shift);
   const int e0 = t * ITEMS - shift;
-  // ignore_eos mask (llm.rs:525-529), softmax (candle softmax_last_dim)
+  // ignore_eos mask (llm.rs:525-529), then candle softmax_last_dim: max,
+  // exp(x - max), sequential f32 sum, divide
   float m = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
@@ -777,32 +783,31 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_cosy(RowArgs a) {
     m = rmaxf(m, x[i]);
   }
   const float mx = block_max(m, s);
-  float part = 0.0f;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    if (!((vm >> i) & 1u)) continue;
-    x[i] = expf_glibc(x[i] - mx);
-    part += x[i];
+  for (int i = 0; i < ITEMS; ++i) x[i] = ((vm >> i) & 1u) ? expf_glibc(x[i] - mx) : 0.0f;
+  auto same = [](float v) { return v; };
+  float S;
+  if (!__builtin_isfinite(mx)) {
+    S = __builtin_nanf("");
+  } else {
+    SeqThread<ITEMS> th;
+    if (!block_seqsum<ITEMS>(x, ~0u, x, same, e0, 0, th, sq, sc, &S))
+      S = block_seqsum_slow<ITEMS>(x, e0, V, s_stage, kMaxVocabReg / 4, &sq.S);
   }
-  const float S = block_sum(part, s);
   put_norm(a, row, S);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) x[i] = x[i] / S;  // probabilities
-  // nucleus (llm.rs:556-592): rank by (prob desc, id asc); at most top_k candidates
+  // nucleus (llm.rs:556-592): candidates are the top_k first under the total
+  // order (prob desc, id asc)
   const uint32_t nvalid = (uint32_t)V;
-  uint32_t K = (a.top_k > 0 && (uint32_t)a.top_k < nvalid) ? (uint32_t)a.top_k : nvalid;
+  const uint32_t K = (a.top_k > 0 && (uint32_t)a.top_k < nvalid) ? (uint32_t)a.top_k : nvalid;
   uint32_t surv = vm;
   if (K < nvalid) {
     uint32_t key[ITEMS];
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
     uint32_t kk;
-    if (block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk)) {
-      surv = 0;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i)
-        if (((vm >> i) & 1u) && key[i] >= kk) surv |= 1u << i;
-    }
+    if (block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk)) surv = block_first_k<ITEMS>(key, vm, kk, K, s);
   }
   const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
   if (n > (uint32_t)kSurvCap) {
@@ -856,31 +861,46 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_cosy(RowArgs a) {
   rep = block_sum_u(rep, s);
   uint32_t tok = top, flags = 0;
   if ((float)rep >= a.ras_thresh) {
-    // random_sample_probs (llm.rs:594-604): sequential CDF over the whole row
+    // random_sample_probs (llm.rs:594-604): acc in vocabulary order over every
+    // probability, first index with pick < acc, else V - 1
     flags = TC_FLAG_RAS;
-    float* stage = reinterpret_cast<float*>(s_seen);
-    constexpr int kChunk = kMaxVocabReg / 4;
     const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row + 1];
-    float acc = 0.0f;
     uint32_t found = 0xffffffffu;
-    for (int c0 = 0; c0 < V; c0 += kChunk) {
+    SeqThread<ITEMS> th;
+    float pv[ITEMS];
 #pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        const int e = e0 + i;
-        if (((vm >> i) & 1u) && e >= c0 && e < c0 + kChunk) stage[e - c0] = x[i];
-      }
-      __syncthreads();
-      if (t == 0 && found == 0xffffffffu) {
-        const int c1 = (c0 + kChunk < V) ? c0 + kChunk : V;
-        for (int e = c0; e < c1; ++e) {
-          acc += stage[e - c0];
-          if (pick < acc) { found = (uint32_t)e; break; }
+    for (int i = 0; i < ITEMS; ++i) pv[i] = ((vm >> i) & 1u) ? x[i] : 0.0f;
+    float Sp;
+    if (block_seqsum<ITEMS>(pv, ~0u, pv, same, e0, 0, th, sq, sc, &Sp)) {
+      float pre[ITEMS];
+      seq_prefix<ITEMS>(th, sq, pre);
+      uint32_t first = 0xffffffffu;
+#pragma unroll
+      for (int i = ITEMS - 1; i >= 0; --i)
+        if (((vm >> i) & 1u) && pick < pre[i]) first = (uint32_t)(e0 + i);
+      found = block_min_u(first, s);
+    } else {
+      constexpr int kChunk = kMaxVocabReg / 4;
+      float acc = 0.0f;
+      for (int c0 = 0; c0 < V; c0 += kChunk) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+          const int e = e0 + i;
+          if (((vm >> i) & 1u) && e >= c0 && e < c0 + kChunk) s_stage[e - c0] = x[i];
         }
-        s_out[2] = found;
+        __syncthreads();
+        if (t == 0 && found == 0xffffffffu) {
+          const int c1 = (c0 + kChunk < V) ? c0 + kChunk : V;
+          for (int e = c0; e < c1; ++e) {
+            acc += s_stage[e - c0];
+            if (pick < acc) { found = (uint32_t)e; break; }
+          }
+          s_out[2] = found;
+        }
+        __syncthreads();
+        found = s_out[2];
+        if (found != 0xffffffffu) break;
       }
-      __syncthreads();
-      found = s_out[2];
-      if (found != 0xffffffffu) break;
     }
     tok = found != 0xffffffffu ? found : (uint32_t)(V - 1);
   }
@@ -947,10 +967,13 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_moss(RowArgs a) {
   for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
   uint32_t kk = 0;
   block_kth_largest<ITEMS>(key, vm, K, s_hist, s, &kk);
-  uint32_t surv = 0;
+  // ranked[0..K) under (value descending, id ascending); more keys equal to
+  // the K-th mean the reference's unstable sort could have kept another id
+  uint32_t ge = 0;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i)
-    if (((vm >> i) & 1u) && key[i] >= kk) surv |= 1u << i;
+  for (int i = 0; i < ITEMS; ++i) ge += (((vm >> i) & 1u) && key[i] >= kk) ? 1u : 0u;
+  const uint32_t n_ge = block_sum_u(ge, s);
+  const uint32_t surv = block_first_k<ITEMS>(key, vm, kk, K, s);
   const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
   if (n > (uint32_t)kSurvCap) {
     finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
@@ -960,9 +983,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_moss(RowArgs a) {
   for (uint32_t j = t; j < n; j += blockDim.x) sv.key[j] = ((uint64_t)(~tkey(sv.val[j])) << 32) | (uint64_t)j;
   __syncthreads();
   sort_survivors(sv, n);
-  // ranked[0..K) = the first K keys; ties beyond K mean the reference's unstable
-  // sort could have kept another id
-  uint32_t flags = n > K ? (uint32_t)TC_FLAG_TIE_CUT : 0u;
+  uint32_t flags = n_ge > K ? (uint32_t)TC_FLAG_TIE_CUT : 0u;
   if (a.greedy) {  // temperature == 0: ranked[0]
     finish_row(a, row, sv.idx[(uint32_t)sv.key[0]], TC_OK, flags);
     no_verify(a, row);

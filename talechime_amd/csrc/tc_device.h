@@ -207,6 +207,51 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, BlockScratch& s,
   return off + inc - v;
 }
 
+__device__ __forceinline__ uint32_t block_min_u(uint32_t v, BlockScratch& s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t w = __shfl_xor(v, o);
+    v = w < v ? w : v;
+  }
+  if (lane_id() == 0) s.u[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = 0xffffffffu;
+  for (int w = 0; w < num_waves(); ++w) r = s.u[w] < r ? s.u[w] : r;
+  __syncthreads();
+  return r;
+}
+
+// The K elements that come first under (key descending, element position
+// ascending), given kk = the K-th largest key: every key above kk, then the
+// keys equal to kk in element order until K are taken.  Returns the mask of
+// taken items.
+template <int ITEMS>
+__device__ __forceinline__ uint32_t block_first_k(const uint32_t (&key)[ITEMS], uint32_t sel, uint32_t kk, uint32_t K,
+                                                  BlockScratch& s) {
+  uint32_t gt = 0, eq = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((sel >> i) & 1u)) continue;
+    gt += key[i] > kk ? 1u : 0u;
+    eq += key[i] == kk ? 1u : 0u;
+  }
+  const uint32_t need = K - block_sum_u(gt, s);
+  uint32_t eq_tot;
+  uint32_t pos = block_excl_scan(eq, s, &eq_tot);
+  uint32_t out = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((sel >> i) & 1u)) continue;
+    if (key[i] > kk) {
+      out |= 1u << i;
+    } else if (key[i] == kk) {
+      if (pos < need) out |= 1u << i;
+      ++pos;
+    }
+  }
+  return out;
+}
+
 // K-th largest (K >= 1) of the 32-bit keys selected by bit i of `sel`.
 // Four MSB-first 8-bit radix passes with LDS histograms.  Returns false when
 // fewer than K keys are selected.

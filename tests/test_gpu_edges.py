@@ -14,6 +14,7 @@ from talechime_amd.sampler import DeviceSampler, launch_shape, make_params  # no
 pytestmark = pytest.mark.gpu
 NEG = -np.inf
 CAP = 64
+KSURV = 1024  # survivors the kernels stage in LDS
 
 
 @pytest.fixture(scope="module")
@@ -25,7 +26,7 @@ def sampler():
     s.close()
 
 
-def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=False, dev_order=True,
+def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=False, dev_order=False,
         hist_mode=0, add_mask=None, pen_mask=None, **kw):
     """Sample with both the GPU and the oracle; returns (gpu dict, oracle dict)."""
     x = np.ascontiguousarray(logits, np.float32)
@@ -401,7 +402,8 @@ def test_indextts_exact_sum_adversarial(sampler):
     for k, p in ((30, 0.8), (2, 0.5), (50, 0.95)):
         g, o = run(sampler, O.INDEXTTS, x, hist, u, temperature=0.8, top_k=k, top_p=p, penalty=1.0, min_keep=2)
         assert np.array_equal(g["norm"].view(np.uint32), o["norm"].view(np.uint32)), (g["norm"], o["norm"])
-        # row 0 ties all 4000 scores: more survivors than the LDS-staged general
-        # path holds (it reports TC_EUNSUPPORTED); its log-sum is still checked
-        assert g["status"][0] == _lib.TC_EUNSUPPORTED
-        same(g, o, rows=range(1, len(rows)), probs_exact=False)
+        # rows whose top-k ties leave more survivors than the LDS stage holds
+        # report TC_EUNSUPPORTED; their log-sums are still checked above
+        big = o["topk_count"] > KSURV
+        assert (g["status"][big] == _lib.TC_EUNSUPPORTED).all()
+        same(g, o, rows=np.nonzero(~big)[0], probs_exact=False)

@@ -2,12 +2,11 @@
 
 Bar: token ids, top-k sets and final candidate sets bit-exact; probabilities
 bit-exact where the arithmetic is order-identical (qwen) and within 1e-5
-relative otherwise.  Rows the reference leaves ambiguous (TC_FLAG_TIE_CUT, NaN
-rows) are counted and excluded.  For the two variants whose reference sums a
-full row sequentially (cosyvoice3 softmax, indextts log_softmax), the device
-sums in a fixed tree order: the GPU must equal the oracle run in that device
-order bit-for-bit, and the rows where that order changes the oracle's own
-answer are the reported boundary rows.
+relative where the device's f64 exp may differ from glibc's in the last f64
+bits.  Rows the reference leaves ambiguous (TC_FLAG_TIE_CUT, NaN rows) are
+counted and excluded.  The full-row sequential f32 sums of the reference
+(indextts log_softmax, cosyvoice3 softmax and fallback CDF) are reproduced
+exactly, so those variants are held to the same bit-exact bar.
 """
 import numpy as np
 import pytest
@@ -83,38 +82,34 @@ def test_indextts_workload_bit_exact(sampler, batch_index):
     assert err < 1e-6
 
 
-@pytest.mark.parametrize("name", ["cosy-ras-128x6564"])
-@pytest.mark.parametrize("batch_index", [0, 1])
-def test_full_row_sum_workloads(sampler, name, batch_index):
-    w = synth.WORKLOADS[name]
+@pytest.mark.parametrize("batch_index", [0, 1, 2])
+def test_cosy_workload_bit_exact(sampler, batch_index):
+    # the softmax denominator and the repetition-window fallback CDF are the
+    # reference's sequential f32 sums: ids, candidate sets and probabilities
+    # equal the reference's bit for bit
+    w = synth.WORKLOADS["cosy-ras-128x6564"]
     b = synth.make_batch(w, batch_index=batch_index)
     g = G.run_gpu(sampler, w, b, CAP)
-    od = G.run_oracle(w, b, CAP, dev_order=G.dev_order_for(w, w.vocab))
-    orf = G.run_oracle(w, b, CAP)
-    assert (g["status"] == 0).all() and (od["status"] == 0).all()
-    # 1. the kernel is exactly the oracle in the device's summation order
-    assert np.array_equal(g["ids"], od["ids"]), np.nonzero(g["ids"] != od["ids"])[0][:10]
-    assert np.array_equal(g["flags"], od["flags"].astype(np.int32))
-    assert not G.set_diff_rows(g, od, CAP)
+    o = G.run_oracle(w, b, CAP)
+    assert (g["status"] == 0).all() and (o["status"] == 0).all()
+    mism = np.nonzero(g["ids"] != o["ids"])[0]
+    bad_sets = G.set_diff_rows(g, o, CAP)
+    _report(w.name, batch=batch_index, rows=w.rows, id_mismatch=len(mism), set_mismatch=len(bad_sets),
+            ras_rows=int(((g["flags"] & 2) != 0).sum()))
+    assert len(mism) == 0, mism[:10]
+    assert not bad_sets, bad_sets[:5]
+    assert np.array_equal(g["flags"], o["flags"].astype(np.int32))
+    assert np.array_equal(g["norm"].view(np.uint32), o["norm"].view(np.uint32))
     n = np.minimum(g["keep_count"], CAP)
     for r in range(w.rows):
-        assert np.array_equal(g["keep_probs"][r, :n[r]], od["keep_probs"][r, :n[r]], equal_nan=True), r
-    # 2. boundary rows: where the summation order alone changes the oracle's token
-    boundary = np.nonzero(od["ids"] != orf["ids"])[0]
-    mism = np.nonzero(g["ids"] != orf["ids"])[0]
-    _report(name, batch=batch_index, rows=w.rows, boundary_rows=len(boundary), id_mismatch_vs_ref=len(mism),
-            ras_rows=int(((g["flags"] & 2) != 0).sum()), prob_rel_err=f"{G.prob_rel_err(g, orf, CAP):.2e}")
-    assert set(mism.tolist()) <= set(boundary.tolist())
-    assert len(boundary) <= max(1, w.rows // 100)
-    # 3. probabilities against the reference order
-    assert G.prob_rel_err(g, orf, CAP) < 1e-5
+        assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
 
 
 def test_cosy_ras_rows_fire(sampler):
     w = synth.WORKLOADS["cosy-ras-128x6564"]
     b = synth.make_batch(w)
     g = G.run_gpu(sampler, w, b, CAP)
-    o = G.run_oracle(w, b, CAP, dev_order=G.dev_order_for(w, w.vocab))
+    o = G.run_oracle(w, b, CAP)
     fired = (g["flags"] & 2) != 0
     assert fired.sum() >= 1
     assert np.array_equal(fired, (o["flags"] & 2) != 0)
