@@ -84,7 +84,10 @@ enum tc_flag {
   TC_FLAG_RAS = 2u,      /* cosyvoice3: the repetition window fired and the second
                             uniform was used (the reference's StepRng advanced twice) */
   TC_FLAG_GREEDY = 4u,   /* qwen: temperature < 0.01, argmax, no uniform used */
-  TC_FLAG_NAN_ROW = 8u   /* qwen: NaN met at top-k (reference order unspecified) */
+  TC_FLAG_NAN_ROW = 8u,  /* qwen: NaN met at top-k (reference order unspecified) */
+  TC_FLAG_NEAR_TIE = 16u /* indextts: a top-p or draw decision lay within the f64 exp
+                            error of the reference's libm (about 2^-46 relative); the
+                            id follows this library's exp */
 };
 
 typedef struct tc_sample_params {

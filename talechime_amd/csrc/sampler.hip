@@ -36,7 +36,7 @@ constexpr int kSurvCap = 1024;      // survivors held in LDS per row
 
 // Register-resident row shapes: ITEMS elements per thread, at most
 // max_threads(ITEMS) threads (which sets the register budget per thread).
-constexpr int max_threads(int items) { return items == 8 ? 1024 : (items == 16 ? 768 : 704); }
+constexpr int max_threads(int items) { return items <= 8 ? 1024 : (items <= 16 ? 768 : 704); }
 
 
 constexpr int kMaxVocabReg = 16384; // register-resident rows: V + alignment <= 1024 * 16
@@ -80,6 +80,7 @@ struct RowArgs {
   int exclude_id;
   int ras_win;
   float ras_thresh;  // (f32)win * tau
+  int fast;          // indextts: the streaming fast path applies (1 <= K <= 64 < V)
 };
 
 struct SurvLds {
@@ -90,6 +91,12 @@ struct SurvLds {
   uint32_t idx[kSurvCap];
   uint8_t flag[kSurvCap];
 };
+
+}  // namespace tc
+
+#include "tc_fast.h"
+
+namespace tc {
 
 // ---------------------------------------------------------------- shared steps
 
@@ -411,188 +418,27 @@ __device__ __forceinline__ float exact_log_softmax(float (&x)[ITEMS], uint32_t v
   return L;
 }
 
-// Candidates held by one wave, two per lane (candidate i in lane i % 64 of
-// slot i / 64), with their rank under (key descending, index descending):
-// rank = number of candidates that beat it.  Counting costs one broadcast per
-// candidate and no shuffles.
-struct WaveCands {
-  uint32_t n;        // candidates (uniform)
-  uint32_t key[2];
-  uint32_t pos[2];   // vocabulary id
-  uint32_t rank[2];
-  bool has[2];
+struct IdxGenLds {
+  uint8_t seen[kMaxVocabReg];
+  SurvLds sv;
+  uint32_t hist[256];
+  BlockScratch s;
+  ScanLds sc;
+  SeqLds sq;
+  uint32_t out[4];
 };
 
-__device__ __forceinline__ void load_wave_cands(const SelLds& sl, uint32_t n_in, WaveCands& c) {
-  const int lane = lane_id();
-  c.n = (uint32_t)__builtin_amdgcn_readfirstlane((int)n_in);
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint32_t i = (uint32_t)(q * kWave + lane);
-    c.has[q] = i < c.n;
-    const uint64_t v = c.has[q] ? candidate_at(sl, i) : 0ull;
-    c.pos[q] = (uint32_t)v;
-    c.key[q] = (uint32_t)(v >> 32);
-    c.rank[q] = 0;
-  }
-  for (uint32_t j = 0; j < c.n; ++j) {
-    const uint32_t kj = readlane_u32(j < 64 ? c.key[0] : c.key[1], j & 63);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint32_t i = (uint32_t)(q * kWave + lane);
-      c.rank[q] += (kj > c.key[q] || (kj == c.key[q] && j > i)) ? 1u : 0u;
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q)
-    if (!c.has[q]) c.rank[q] = 0xffffffffu;
-}
-
-// Candidate index (uniform) holding rank r.
-__device__ __forceinline__ uint32_t cand_of_rank(const WaveCands& c, uint32_t r) {
-  const uint64_t b0 = __ballot(c.rank[0] == r), b1 = __ballot(c.rank[1] == r);
-  return b0 ? (uint32_t)__builtin_ctzll(b0) : 64u + (uint32_t)__builtin_ctzll(b1);
-}
-
-__device__ __forceinline__ double pick_d(const double (&v)[2], uint32_t i) {
-  return readlane_f64(i < 64 ? v[0] : v[1], i & 63);
-}
-
-// One-wave finish of an indextts row over its n <= SelLds::kCapF top-k
-// candidates (vocabulary order in the wave regions): top-k cut, top-p
-// (generation.rs:169-194), then one draw of sample_without_replacement
-// (generation.rs:280-303).  All scores are finite here.
-__device__ __forceinline__ void indextts_finish(const RowArgs& a, int row, const SelLds& sl, uint32_t n_in) {
-  const int lane = lane_id();
-  WaveCands c;
-  load_wave_cands(sl, n_in, c);
-  float sc[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) sc[q] = untkey(c.key[q]);
-  const uint32_t K = (uint32_t)a.K;
-  const uint32_t ik = cand_of_rank(c, K - 1);
-  const float kth = untkey(readlane_u32(ik < 64 ? c.key[0] : c.key[1], ik & 63));
-  bool surv[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) surv[q] = c.has[q] && !(sc[q] < kth);
-  const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
-  const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
-  uint64_t rm0 = 0, rm1 = 0;
-  if (a.do_topp) {
-    // f64 softmax over the row: removed entries are -inf and add exact zeros
-    const uint32_t i0 = cand_of_rank(c, 0);
-    const double mxd = (double)readlane_f32(i0 < 64 ? sc[0] : sc[1], i0 & 63);
-    double w[2], p[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
-    double sum = -0.0;
-    for (uint64_t m = sm0; m; m &= m - 1) sum += readlane_f64(w[0], __builtin_ctzll(m));
-    for (uint64_t m = sm1; m; m &= m - 1) sum += readlane_f64(w[1], __builtin_ctzll(m));
-#pragma unroll
-    for (int q = 0; q < 2; ++q) p[q] = w[q] / sum;
-    // ascending stable order = ranks from the last survivor back to 0
-    double cum = 0.0;
-    const double lim = 1.0 - a.top_p_d;
-    for (int r = (int)ns - 1; r >= 0; --r) {
-      const uint32_t i = cand_of_rank(c, (uint32_t)r);
-      cum += pick_d(p, i);
-      if (cum <= lim) {
-        if (i < 64) rm0 |= 1ull << i;
-        else rm1 |= 1ull << (i - 64);
-      }
-    }
-    for (uint32_t r = 0; r < ns && r < (uint32_t)a.min_keep; ++r) {
-      const uint32_t i = cand_of_rank(c, r);
-      if (i < 64) rm0 &= ~(1ull << i);
-      else rm1 &= ~(1ull << (i - 64));
-    }
-  }
-  const uint64_t lm0 = sm0 & ~rm0, lm1 = sm1 & ~rm1;
-  bool live[2];
-  live[0] = (lm0 >> lane) & 1ull;
-  live[1] = (lm1 >> lane) & 1ull;
-  const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
-  // the draw: softmax over the live entries in vocabulary order
-  double ml = -__builtin_inf();
-#pragma unroll
-  for (int q = 0; q < 2; ++q)
-    if (live[q]) ml = rmaxd(ml, (double)sc[q] + 0.0);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ml = rmaxd(ml, __shfl_xor(ml, o));
-  double ev[2], wv[2], acc[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    ev[q] = live[q] ? tc_exp_d(((double)sc[q] + 0.0) - ml) : 0.0;
-    acc[q] = 0.0;
-  }
-  double sum2 = -0.0;
-  for (uint64_t m = lm0; m; m &= m - 1) sum2 += readlane_f64(ev[0], __builtin_ctzll(m));
-  for (uint64_t m = lm1; m; m &= m - 1) sum2 += readlane_f64(ev[1], __builtin_ctzll(m));
-#pragma unroll
-  for (int q = 0; q < 2; ++q) wv[q] = live[q] ? ev[q] / sum2 : 0.0;
-  // inverse_cdf: the running sum is also `total` (zero weights add nothing)
-  double run = 0.0;
-  for (uint64_t m = lm0; m; m &= m - 1) {
-    const int l = __builtin_ctzll(m);
-    run += readlane_f64(wv[0], l);
-    if (lane == l) acc[0] = run;
-  }
-  for (uint64_t m = lm1; m; m &= m - 1) {
-    const int l = __builtin_ctzll(m);
-    run += readlane_f64(wv[1], l);
-    if (lane == l) acc[1] = run;
-  }
-  const double uu = reinterpret_cast<const double*>(a.uniforms)[row] * run;
-  const uint64_t hit0 = __ballot(live[0] && wv[0] > 0.0 && acc[0] > uu);
-  const uint64_t hit1 = __ballot(live[1] && wv[1] > 0.0 && acc[1] > uu);
-  const uint64_t pz0 = __ballot(live[0] && wv[0] > 0.0), pz1 = __ballot(live[1] && wv[1] > 0.0);
-  uint32_t pick;
-  if (hit0) pick = (uint32_t)__builtin_ctzll(hit0);
-  else if (hit1) pick = 64 + (uint32_t)__builtin_ctzll(hit1);
-  else if (pz1) pick = 64 + 63 - (uint32_t)__builtin_clzll(pz1);
-  else if (pz0) pick = 63 - (uint32_t)__builtin_clzll(pz0);
-  else pick = lm0 ? (uint32_t)__builtin_ctzll(lm0) : 64 + (uint32_t)__builtin_ctzll(lm1);
-  const uint32_t tok = nl ? readlane_u32(pick < 64 ? c.pos[0] : c.pos[1], pick & 63) : 0u;
-  if (lane == 0) {
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = nl ? TC_OK : TC_ETOOFEW;
-    if (a.out_flags) a.out_flags[row] = 0u;
-    if (a.topk_count) {
-      a.topk_count[row] = ns;
-      a.keep_count[row] = nl;
-    }
-  }
-  if (a.topk_count) {
-    const uint64_t below = (1ull << lane) - 1ull;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const uint64_t smq = q == 0 ? sm0 : sm1, lmq = q == 0 ? lm0 : lm1;
-      const uint32_t so = q == 0 ? 0u : (uint32_t)__popcll(sm0), lo = q == 0 ? 0u : (uint32_t)__popcll(lm0);
-      if (surv[q]) {
-        const uint32_t j = so + (uint32_t)__popcll(smq & below);
-        if (j < a.cap) a.topk_ids[(size_t)row * a.cap + j] = c.pos[q];
-      }
-      if (live[q]) {
-        const uint32_t j = lo + (uint32_t)__popcll(lmq & below);
-        if (j < a.cap) {
-          a.keep_ids[(size_t)row * a.cap + j] = c.pos[q];
-          a.keep_probs[(size_t)row * a.cap + j] = (float)wv[q];
-        }
-      }
-    }
-  }
-}
-
+// General path: any K, non-finite scores, more candidates than the fast path
+// stages.  Survivors of the top-k cut are staged in LDS (at most kSurvCap).
 template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
-  __shared__ uint8_t s_seen[kMaxVocabReg];
-  __shared__ SurvLds sv;
-  __shared__ uint32_t s_hist[256];
-  __shared__ BlockScratch s;
-  __shared__ ScanLds sc;
-  __shared__ SeqLds sq;
-  __shared__ SelLds sl;
-  __shared__ uint32_t s_out[4];
+__device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
+  uint8_t* s_seen = G.seen;
+  SurvLds& sv = G.sv;
+  uint32_t* s_hist = G.hist;
+  BlockScratch& s = G.s;
+  ScanLds& sc = G.sc;
+  SeqLds& sq = G.sq;
+  uint32_t* s_out = G.out;
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
   float x[ITEMS];
@@ -611,31 +457,6 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
     if (a.do_pen && s_seen[e0 + i]) v = v < 0.0f ? v * a.pen_f : v / a.pen_f;
     if (a.do_temp) v = v / a.t_f;
     x[i] = v;
-  }
-  // fast path: top-k of at most 64 with every score finite -> candidates from
-  // the per-thread-maximum bound, finished by one wave
-  if (a.K > 0 && a.K <= 64 && a.K < V) {
-    uint32_t key[ITEMS];
-    uint32_t nf = 0;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const bool v = (vm >> i) & 1u;
-      key[i] = v ? tkey(x[i]) : 0u;
-      nf |= (v && !__builtin_isfinite(x[i])) ? 1u : 0u;
-    }
-    uint32_t T0 = block_topk_bound<ITEMS>(key, vm, a.K, sl);
-    if (T0 == 0x80000000u) T0 = 0x7fffffffu;  // -0.0 compares equal to a +0.0 cut
-    uint32_t sel = 0;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i)
-      if (((vm >> i) & 1u) && key[i] >= T0) sel |= 1u << i;
-    bool of;
-    uint32_t nfl;
-    const uint32_t n = block_compact_candidates<ITEMS>(key, sel, e0, sl, nf != 0u, &of, &nfl);
-    if (!of && !nfl && n <= (uint32_t)SelLds::kCapF) {
-      if (wave_id() == 0) indextts_finish(a, row, sl, n);
-      return;
-    }
   }
   // general path: radix select over the whole row, survivors staged in LDS
   float kth = -__builtin_inff();
@@ -751,6 +572,167 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       a.keep_count[row] = c;
     }
   }
+}
+
+struct IdxFastLds {
+  uint32_t bits[kMaxVocabReg / 32];  // history ids present (bit per id)
+  uint32_t bins[64];                 // thread maxima of d per 0.25-wide bucket below the row max
+  float wmax[kMaxWaves];
+  float wfin[kMaxWaves];
+  uint32_t wcand[kMaxWaves];
+  SeqFastLds seq;
+  FinLds fin;
+};
+// The fast path hands a row to the general path before the general path
+// touches LDS, so the two share it.
+union IdxLds {
+  IdxFastLds f;
+  IdxGenLds g;
+};
+
+// indextts (generation.rs:643-676 with one draw, 280-303).  Fast path for
+// 1 <= K <= 64 < V on rows whose logits are all finite: the row is streamed
+// once into registers with the history ids in flight beside it;
+// log_softmax's sequential f32 denominator is reproduced exactly
+// (block_seqsum_fast); the K-th largest penalised log-prob x' is bounded from
+// below by a histogram of the per-thread maxima of d = x - max over ids not
+// in the history (x' = d - L is monotone in d for them), and every element
+// whose x' lies within a quarter nat of that bound becomes a candidate -- a
+// margin far wider than the few floats the later division by T can round
+// together.  One wave finishes the row.  Everything else takes idx_general.
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
+  __shared__ IdxLds U;
+  IdxFastLds& F = U.f;
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  if (a.fast) {
+    const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+    float x[ITEMS];
+    int shift;
+    load_row<ITEMS>(rp, V, x, &shift);
+    // history ids: up to kHpt per thread in flight with the row
+    constexpr int kHpt = 4;
+    uint32_t h0 = 0, h1 = 0;
+    if (a.do_pen) hist_range(a, row, &h0, &h1);
+    uint32_t hid[kHpt];
+#pragma unroll
+    for (int j = 0; j < kHpt; ++j) {
+      const uint32_t k = h0 + (uint32_t)t + (uint32_t)j * blockDim.x;
+      hid[j] = k < h1 ? a.hist_ids[k] : 0xffffffffu;
+    }
+    const int nwords = (V + 31) >> 5;
+    for (int w = t; w < nwords; w += blockDim.x) F.bits[w] = 0u;
+    if (t < 64) F.bins[t] = 0u;
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < kHpt; ++j)
+      if (hid[j] < (uint32_t)V) atomicOr(&F.bits[hid[j] >> 5], 1u << (hid[j] & 31u));
+    for (uint32_t k = h0 + (uint32_t)t + (uint32_t)kHpt * blockDim.x; k < h1; k += blockDim.x) {
+      const uint32_t id = a.hist_ids[k];
+      if (id < (uint32_t)V) atomicOr(&F.bits[id >> 5], 1u << (id & 31u));
+    }
+    const uint32_t vm = valid_mask<ITEMS>(V, shift);
+    const int e0 = t * ITEMS - shift;
+    // row max; the sum of the row is finite iff every logit is (or overflows:
+    // then the general path)
+    float m = -__builtin_inff(), fsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((vm >> i) & 1u) {
+        m = m > x[i] ? m : x[i];
+        fsum += x[i];
+      }
+    m = dpp_wave_max(m);
+    fsum = dpp_wave_sum(fsum);
+    if (lane_id() == 0) {
+      F.wmax[wave_id()] = m;
+      F.wfin[wave_id()] = fsum;
+    }
+    lds_barrier();
+    float mx = F.wmax[0], fin = 0.0f;
+    for (int w = 0; w < num_waves(); ++w) {
+      mx = mx > F.wmax[w] ? mx : F.wmax[w];
+      fin += F.wfin[w];
+    }
+    if (__builtin_isfinite(fin) && __builtin_isfinite(mx)) {
+      // ids in the history, bit i = element e0 + i
+      uint64_t seen = 0;
+      if (a.do_pen) {
+        const int w0 = e0 >= 0 ? (e0 >> 5) : 0;
+        const uint32_t lo = w0 < nwords ? F.bits[w0] : 0u;
+        const uint32_t hi = w0 + 1 < nwords ? F.bits[w0 + 1] : 0u;
+        seen = ((((uint64_t)hi << 32) | lo) >> (e0 >= 0 ? (e0 & 31) : 0));
+        if (e0 < 0) seen <<= (uint32_t)(-e0);
+      }
+      // log_softmax (generation.rs:95-105): d = x - max; S = sequential f32 sum of exp(d)
+      float d[ITEMS], ap[ITEMS];
+      uint32_t exm = 0, force = 0;
+      float mns = -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const bool v = (vm >> i) & 1u;
+        d[i] = x[i] - mx;
+        if (v && !((seen >> i) & 1ull)) mns = mns > d[i] ? mns : d[i];
+        ap[i] = v ? exp_approx(d[i]) : 0.0f;
+        exm |= (v ? 0u : 1u) << i;
+        force |= (v && !(d[i] >= -87.0f) ? 1u : 0u) << i;  // below the approximation's range
+      }
+      if (mns > -16.0f) atomicAdd(&F.bins[(uint32_t)(-mns * 4.0f)], 1u);
+      bool ok = true;
+      float S = block_seqsum_fast<ITEMS>(ap, exm, force, d, [](float v) { return expf_glibc(v); }, e0, F.seq, &ok);
+      if (!ok) {
+        float ex[ITEMS];
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) ex[i] = ((vm >> i) & 1u) ? expf_glibc(d[i]) : 0.0f;
+        __syncthreads();
+        S = block_seqsum_slow<ITEMS>(ex, e0, V, F.seq.x, SeqFastLds::kCap, &F.seq.S);
+      }
+      const float L = logf_glibc(S);
+      put_norm(a, row, L);
+      // the bucket of the K-th largest thread maximum (the histogram is complete
+      // after the first barrier in block_seqsum_fast)
+      const uint32_t cum = dpp_scan_u32(F.bins[lane_id()]);
+      const uint64_t reach = __ballot(cum >= (uint32_t)a.K);
+      if (reach) {
+        // the K-th largest x' is at least fl(-(b0 + 1) / 4 - L); 2^-10 covers the
+        // roundings of that bound and the floats the division by T merges
+        const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
+        const float thr = (-(float)(b0 + 1u) * 0.25f - L) - 0x1p-10f;
+        // x' = (x - max) - L; repetition penalty on the log-probs
+        // (generation.rs:122-134): x' <= 0 here (L = ln S >= 0), where
+        // s < 0 ? s * pen : s / pen equals s * pen, signed zeros included
+        uint64_t key[ITEMS];
+        uint32_t sel = 0;
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+          float v = d[i] - L;
+          v = ((seen >> i) & 1ull) ? v * a.pen_f : v;
+          key[i] = ((uint64_t)tkey(v) << 32) | (uint32_t)(e0 + i);
+          sel |= ((((vm >> i) & 1u) && v >= thr) ? 1u : 0u) << i;
+        }
+        const uint32_t c = (uint32_t)__builtin_popcount(sel);
+        const uint32_t ci = dpp_scan_u32(c);
+        if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
+        lds_barrier();
+        uint32_t off = ci - c, n = 0;
+        for (int w = 0; w < num_waves(); ++w) {
+          const uint32_t cw = F.wcand[w];
+          off += w < wave_id() ? cw : 0u;
+          n += cw;
+        }
+        if (n <= (uint32_t)FinLds::kCap) {
+#pragma unroll
+          for (int i = 0; i < ITEMS; ++i)
+            if ((sel >> i) & 1u) F.fin.cand[off++] = key[i];
+          lds_barrier();
+          if (wave_id() == 0) idx_fast_finish(a, row, n, F.fin);
+          return;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  idx_general<InT, ITEMS>(a, U.g);
 }
 
 // ================================================================ cosyvoice3
@@ -1296,19 +1278,25 @@ struct DeviceGuard {
   }
 };
 
-// Block shape for a register-resident row: ITEMS per thread, threads a
-// multiple of 64 in [256, 1024].
+// Block shape for a register-resident row: ITEMS consecutive elements per
+// thread (a multiple of the 16-byte load width), threads a multiple of 64 in
+// [256, 1024]; rounded up to a multiple of 256 (four waves, one per SIMD) when
+// that still fits, so the SIMDs share the row evenly.
 bool pick_shape(int V, int dtype, int* items, int* threads) {
   const int pad = dtype == TC_BF16 ? 7 : 3;
-  for (int it : {8, 16, 24}) {
+  static const int f32_items[] = {8, 12, 16, 24}, bf16_items[] = {8, 16, 24};
+  const int* its = dtype == TC_BF16 ? bf16_items : f32_items;
+  const int n_its = dtype == TC_BF16 ? 3 : 4;
+  for (int k = 0; k < n_its; ++k) {
+    const int it = its[k];
     int nt = (V + pad + it - 1) / it;
     nt = (nt + 63) / 64 * 64;
     if (nt < 256) nt = 256;
-    if (nt <= tc::max_threads(it)) {
-      *items = it;
-      *threads = nt;
-      return true;
-    }
+    if (nt > tc::max_threads(it)) continue;
+    const int bal = (nt + 255) / 256 * 256;
+    *items = it;
+    *threads = bal <= tc::max_threads(it) ? bal : nt;
+    return true;
   }
   return false;
 }
@@ -1319,6 +1307,7 @@ bool pick_shape(int V, int dtype, int* items, int* threads) {
     dim3 g(rows), b(threads);                                                                    \
     if (dtype == TC_F32) {                                                                       \
       if (items == 8) hipLaunchKernelGGL((tc::NAME<float, 8>), g, b, 0, st, a);                  \
+      else if (items == 12) hipLaunchKernelGGL((tc::NAME<float, 12>), g, b, 0, st, a);           \
       else if (items == 16) hipLaunchKernelGGL((tc::NAME<float, 16>), g, b, 0, st, a);           \
       else hipLaunchKernelGGL((tc::NAME<float, 24>), g, b, 0, st, a);                            \
     } else {                                                                                     \
@@ -1455,6 +1444,7 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
       }
       a.do_topp = p->top_p < 1.0;
       a.top_p_d = p->top_p;
+      a.fast = a.K >= 1 && a.K <= 64 && a.K < V && a.min_keep <= a.K;
       break;
     }
     case TC_MOSS: {
@@ -1590,6 +1580,7 @@ int tc_greedy_sample(const void* d_logits, int dtype, size_t rows, size_t vocab,
   dim3 g((unsigned)rows), b(threads);
   if (dtype == TC_F32) {
     if (items == 8) hipLaunchKernelGGL((tc::k_greedy<float, 8>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
+    else if (items == 12) hipLaunchKernelGGL((tc::k_greedy<float, 12>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
     else if (items == 16) hipLaunchKernelGGL((tc::k_greedy<float, 16>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
     else hipLaunchKernelGGL((tc::k_greedy<float, 24>), g, b, 0, st, (const float*)d_logits, (long long)ld, (int)vocab, d_out_ids);
   } else {

@@ -1,0 +1,462 @@
+// tc_fast.h -- the streaming fast path of the indextts sampler: an LDS-only
+// barrier, an exact emulation of a sequential f32 sum classified in f32
+// arithmetic, and a one-wave finish whose order-dependent f64 sums are wave
+// scans with a rigorous error margin, falling back to the reference's
+// sequential loops when a decision lies inside that margin.  Cross-lane
+// traffic uses DPP (tc_dpp.h).
+#pragma once
+
+#include "tc_device.h"
+#include "tc_dpp.h"
+#include "tc_select.h"
+
+namespace tc {
+
+// Barrier that waits only for this thread's LDS operations: global loads
+// issued before it stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+__device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// exp(d) for d in [-87, 0]: tc_expf_fast, within 1 ulp of the correctly
+// rounded value (checked for every input by the table generator); glibc's
+// expf is within 1 ulp of it too, so kSeqErr = 2^-21 bounds the relative
+// distance from the reference's term with a margin of 2.
+__device__ __forceinline__ float exp_approx(float d) { return tc_expf_fast(d); }
+
+// ---------------------------------------------------------------- exact sequential sum
+// The bits of s = -0.0f; for each term in element order: s = s + t (the
+// reference's softmax denominators).  The running sum is predicted from
+// approximate terms (relative error <= kSeqErr) with a bound `tau` on its
+// distance from the true sequential sum.  An element whose sum before and
+// after provably stays in one binade [2^e, 2^(e+1)) adds round(t / 2^(e-23))
+// ulps, an integer; when the approximate term cannot settle that rounding
+// the exact term is computed.  Ties, binade crossings and the first positive
+// term go to a list that one wave replays exactly.  The integer
+// contributions are summed modulo 2^32: between two listed elements they stay
+// inside one binade, so every difference the replay takes is below 2^24.
+constexpr float kSeqErr = 0x1p-21f;
+
+struct SeqFastLds {
+  static constexpr int kCap = 512;
+  float x[kCap];      // listed element: its input (exact term not yet known) or its exact term
+  float P[kCap];      // the prediction of the running sum before it
+  uint32_t q[kCap];   // integer contributions of the safe elements before it (mod 2^32)
+  uint32_t info[kCap];  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: position
+  float wsum[kMaxWaves];
+  uint32_t wcnt[kMaxWaves];
+  uint32_t wq[kMaxWaves];
+  float S;
+  uint32_t bad;
+};
+
+// Classification of one element, without branches: 0 = safe (*r set: the
+// element adds *r ulps of its binade), 1 = the approximate term cannot decide
+// the rounding, 2 = listed (first positive term, binade crossing, tie, or a
+// running sum outside [2^-104, 2^23)).
+__device__ __forceinline__ uint32_t seq_classify(float P, float Pn, float a, bool exact, float m_lo, float m_hi,
+                                                 uint32_t* r) {
+  const uint32_t pb = __float_as_uint(P);
+  const bool ok_p = P > 0.0f && pb >= 0x0b800000u && pb < 0x4b000000u;
+  const uint32_t eb = ok_p ? (pb & 0x7f800000u) : 0x3f800000u;
+  const float lo = __uint_as_float(eb), hi = __uint_as_float(eb + 0x00800000u);
+  const bool inb = ok_p && P * m_lo >= lo && Pn * m_hi < hi;
+  const float q = a * __uint_as_float(0x8a800000u - eb);  // a / 2^(e-23), exact
+  const float fl = __builtin_floorf(q), fr = q - fl;
+  const bool amb = !exact && __builtin_fabsf(fr - 0.5f) <= q * (2.0f * kSeqErr) + 0x1p-24f;
+  const bool zero = exact && a == 0.0f;
+  *r = zero ? 0u : (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+  return zero ? 0u : (!inb ? 2u : (amb ? 1u : (fr == 0.5f ? 2u : 0u)));
+}
+
+// |true sequential sum - prediction| <= tau * prediction for an element at
+// position pos: sequential rounding (pos * 2^-24), the approximate terms
+// (kSeqErr), the prediction's own f32 adds (at most ITEMS + 6 + 16) and the
+// f32 products in the binade tests.
+__device__ __forceinline__ float seq_tau(int pos) {
+  return (float)(pos + 64) * 0x1p-24f * 1.01f + kSeqErr + 0x1p-21f;
+}
+
+// The exact term of one element from its input (the caller's functor) with
+// the correctly rounded exp computed in place: f(x) is the reference's term.
+// Thread t holds ITEMS terms at element positions pos0 + i (threads in order,
+// positions increasing).  ap[i]: the term, exact where bit i of `exact_mask`
+// is set (invalid positions: an exact 0), otherwise within kSeqErr of f(x[i]),
+// the exact term; bits of `force` are treated as undecided whatever ap holds.
+// LDS writes the caller issued before the call are complete and visible after
+// its first barrier.  Returns the sum, or sets *ok = false when more than kCap
+// elements need the replay or the replay met an inconsistency (the caller
+// then sums literally).  Every thread of the block must call it.
+template <int ITEMS, class F>
+__device__ __forceinline__ float block_seqsum_fast(const float (&ap)[ITEMS], uint32_t exact_mask, uint32_t force,
+                                                   const float (&x)[ITEMS], F f, int pos0, SeqFastLds& L, bool* ok) {
+  const int lane = lane_id(), wv = wave_id();
+  // 1. prediction: f32 partial sums, exclusive prefix over threads
+  float D = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) D += ap[i];
+  const float inc = dpp_scan_f32(D);
+  const float ex = dpp_prev_f32(inc);  // earlier lanes of this wave
+  if (lane == kWave - 1) L.wsum[wv] = inc;
+  lds_barrier();
+  float off = 0.0f;
+  for (int w = 0; w < wv; ++w) off += L.wsum[w];
+  const float P0 = off + ex;
+  const float tau = seq_tau(pos0 + ITEMS);
+  const float m_lo = 1.0f - tau, m_hi = 1.0f + tau;
+  // 2. classify with the terms at hand; undecided and listed elements go to
+  // the replay list
+  uint32_t r[ITEMS];
+  uint32_t unsafe = 0, amb = force;
+  {
+    float P = P0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      const float Pn = P + ap[i];
+      const uint32_t c = seq_classify(P, Pn, ap[i], (exact_mask >> i) & 1u, m_lo, m_hi, &r[i]);
+      amb |= (c == 1u ? 1u : 0u) << i;
+      unsafe |= (c == 2u ? 1u : 0u) << i;
+      P = Pn;
+    }
+  }
+  amb &= ~unsafe;
+  const uint32_t listed = unsafe | amb;
+  uint32_t rsum = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) rsum += ((listed >> i) & 1u) ? 0u : r[i];
+  // 3. the list in element order: exclusive scan of (count, rsum)
+  const uint32_t cnt = (uint32_t)__builtin_popcount(listed);
+  const uint32_t ci = dpp_scan_u32(cnt), qi = dpp_scan_u32(rsum);
+  if (lane == kWave - 1) {
+    L.wcnt[wv] = ci;
+    L.wq[wv] = qi;
+  }
+  lds_barrier();
+  uint32_t c_off = ci - cnt, q_off = qi - rsum, c_tot = 0, q_tot = 0;
+  for (int w = 0; w < num_waves(); ++w) {
+    const uint32_t wc = L.wcnt[w], wq = L.wq[w];
+    if (w < wv) {
+      c_off += wc;
+      q_off += wq;
+    }
+    c_tot += wc;
+    q_tot += wq;
+  }
+  if (c_tot > (uint32_t)SeqFastLds::kCap) {
+    *ok = false;
+    return 0.0f;
+  }
+  if (listed) {
+    uint32_t k = c_off, q = q_off;
+    float P = P0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if ((listed >> i) & 1u) {
+        const bool exa = (exact_mask >> i) & 1u;
+        L.x[k] = exa ? ap[i] : x[i];
+        L.P[k] = P;
+        L.q[k] = q;
+        L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | ((uint32_t)(pos0 + i) << 8);
+        ++k;
+      } else {
+        q += r[i];
+      }
+      P = P + ap[i];
+    }
+  }
+  lds_barrier();
+  // 4. the replay (wave 0): per chunk of 64 listed elements, the exact terms
+  // in parallel, the undecided ones classified again (those that turn out
+  // safe fold into the integer contributions), then one walk over the rest
+  if (wv == 0) {
+    float s = -0.0f;
+    uint32_t qp = 0, bad = 0, fold = 0;
+    for (uint32_t base = 0; base < c_tot; base += kWave) {
+      const uint32_t k = base + (uint32_t)lane;
+      const bool in = k < c_tot;
+      const uint32_t info = in ? L.info[k] : 1u;
+      const float xin = in ? L.x[k] : 0.0f;
+      const float Pk = in ? L.P[k] : 0.0f;
+      const float a = (info & 1u) ? xin : f(xin);
+      uint32_t rk = 0;
+      const float tk = seq_tau((int)(info >> 8));
+      const bool safe = in && (info & 2u) && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
+      const uint32_t rs = safe ? rk : 0u;
+      const uint32_t R = dpp_scan_u32(rs) + fold;  // folded contributions up to and including k
+      const uint32_t qk = (in ? L.q[k] : 0u) + (R - rs);
+      fold = rl_u32(R, kWave - 1);
+      uint64_t walk = __ballot(in && !safe);
+      while (walk) {
+        const int j = __builtin_ctzll(walk);
+        walk &= walk - 1;
+        const uint32_t qj = rl_u32(qk, j);
+        const float aj = rl_f32(a, j);
+        const uint32_t d = qj - qp;
+        const float s2 = u2f(f2u(s) + d);
+        bad |= (d != 0u && (!(s > 0.0f) || (f2u(s2) >> 23) != (f2u(s) >> 23))) ? 1u : 0u;
+        s = (d != 0u ? s2 : s) + aj;
+        qp = qj;
+      }
+    }
+    const uint32_t d = q_tot + fold - qp;
+    if (d != 0u) {
+      const float s2 = u2f(f2u(s) + d);
+      if (!(s > 0.0f) || (f2u(s2) >> 23) != (f2u(s) >> 23)) bad = 1u;
+      s = s2;
+    }
+    if (lane == 0) {
+      L.S = s == 0.0f ? 0.0f : s;  // the terms are +0 or positive: a zero sum is +0
+      L.bad = bad;
+    }
+  }
+  lds_barrier();
+  *ok = L.bad == 0u;
+  return L.S;
+}
+
+// ---------------------------------------------------------------- one-wave finish (indextts)
+// Relative distance within which a comparison of two f64 sums of n
+// non-negative terms may differ between a tree order and the reference's
+// sequential order (n * 2^-52 for the orders, a few roundings for the
+// divisions and the scan's own error), plus the difference the f64 exp of this
+// library may have from the reference's libm (tc_exp_d is within 2^-49).
+__device__ __forceinline__ double order_margin(uint32_t n) { return (double)(8u * n + 96u) * 0x1p-53 + 0x1p-46; }
+__device__ __forceinline__ double exp_margin() { return 0x1p-46; }
+
+struct FinLds {
+  static constexpr int kCap = 128;
+  uint64_t cand[kCap];     // (tkey(x'), id) in vocabulary order
+  uint32_t rank_of[kCap];  // rank (value descending, id descending) of vocabulary-order candidate c
+  double pr[kCap];         // by rank: top-p probability
+};
+
+// The reference's order for an ascending cumulative walk and the draw, one
+// lane walking uniform loops; used when a wave-scan decision is too close to
+// call.
+__device__ __forceinline__ uint32_t idx_topp_cut_exact(const double (&w)[2], uint64_t sm0, uint64_t sm1,
+                                                       const uint64_t (&srt)[2], uint32_t ns, double lim, bool* near) {
+  double sr = -0.0;
+  for (uint64_t m = sm0; m; m &= m - 1) sr += rl_f64(w[0], __builtin_ctzll(m));
+  for (uint64_t m = sm1; m; m &= m - 1) sr += rl_f64(w[1], __builtin_ctzll(m));
+  double cum = 0.0;
+  uint32_t rc = ns;
+  for (int p = (int)ns - 1; p >= 0; --p) {
+    const uint32_t c = (uint32_t)rl_u32((uint32_t)(p < 64 ? srt[0] : srt[1]), p & 63);
+    const double wc = rl_f64(c < 64 ? w[0] : w[1], (int)(c & 63u));
+    cum += wc / sr;
+    if (__builtin_fabs(cum - lim) <= exp_margin() * (cum > lim ? cum : lim)) *near = true;
+    if (cum <= lim) rc = (uint32_t)p;
+  }
+  return rc;
+}
+
+// One-wave finish of an indextts row from its n (K <= n <= 128) candidates
+// (F.cand, vocabulary order; the scores before the division by T): the
+// top-k cut (generation.rs:148-161), top-p (169-194) and one draw of
+// sample_without_replacement (280-303) on x'' = x' / T.  Every element whose
+// score can reach the k-th largest is a candidate; all scores are finite.
+__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, FinLds& F) {
+  const int lane = lane_id();
+  float sc[2];
+  uint32_t id[2];
+  bool has[2];
+  uint64_t srt[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t c = (uint32_t)(q * kWave + lane);
+    has[q] = c < n;
+    const uint64_t v = has[q] ? F.cand[c] : 0ull;
+    id[q] = (uint32_t)v;
+    const float xp = untkey((uint32_t)(v >> 32));
+    sc[q] = a.do_temp ? xp / a.t_f : xp;
+    // rank key: value descending, then the later id first (the reverse of the
+    // reference's ascending stable order)
+    srt[q] = has[q] ? (((uint64_t)tkey(sc[q]) << 32) | c) : 0ull;
+  }
+  if (n <= (uint32_t)kWave) {
+    uint64_t one[1] = {srt[0]};
+    dpp_sort_desc_u64<1>(one);
+    srt[0] = one[0];
+    srt[1] = 0ull;
+  } else {
+    dpp_sort_desc_u64<2>(srt);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t p = (uint32_t)(q * kWave + lane);
+    if (p < n) F.rank_of[(uint32_t)srt[q]] = p;
+  }
+  lds_wait();
+  uint32_t rk[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) rk[q] = has[q] ? F.rank_of[q * kWave + lane] : 0xffffffffu;
+  const uint32_t K = (uint32_t)a.K;
+  const float kth = untkey(rl_u32((uint32_t)((K - 1) < 64 ? srt[0] >> 32 : srt[1] >> 32), (int)((K - 1) & 63)));
+  const float vmax = untkey(rl_u32((uint32_t)(srt[0] >> 32), 0));
+  bool surv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) surv[q] = has[q] && !(sc[q] < kth);
+  const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
+  const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  uint32_t flags = 0;
+  // ---- top-p: ranks [r_cut, ns) are removed, except the min_keep first
+  uint32_t r_cut = ns;
+  if (a.do_topp) {
+    const double mxd = (double)vmax;
+    double w[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
+    const double sum = dpp_wave_sum_d(w[0] + w[1]);
+    const double rsum = 1.0 / sum;  // within the margin: a product with the reciprocal
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (surv[q]) F.pr[rk[q]] = w[q] * rsum;
+    lds_wait();
+    // ascending position a = rank ns-1-a; cum(a) is the reference's running sum
+    // after adding position a
+    double pa[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ap = (uint32_t)(q * kWave + lane);
+      pa[q] = ap < ns ? F.pr[ns - 1u - ap] : 0.0;
+    }
+    const double c0 = dpp_scan_f64(pa[0]);
+    const double c1 = dpp_scan_f64(pa[1]) + rl_f64(c0, kWave - 1);
+    const double lim = 1.0 - a.top_p_d;
+    const uint64_t rm0 = __ballot((uint32_t)lane < ns && c0 <= lim);
+    const uint64_t rm1 = __ballot((uint32_t)(kWave + lane) < ns && c1 <= lim);
+    const uint32_t n_rm = (uint32_t)(__popcll(rm0) + __popcll(rm1));
+    r_cut = ns - n_rm;
+    // the decisions at the last removed and the first kept positions
+    const double mg = order_margin(ns);
+    bool close = false;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ap = (uint32_t)(q * kWave + lane);
+      const double cq = q == 0 ? c0 : c1;
+      if (ap < ns && (ap + 1u == n_rm || ap == n_rm) && __builtin_fabs(cq - lim) <= mg * (cq > lim ? cq : lim))
+        close = true;
+    }
+    if (__ballot(close)) {
+      bool near = false;
+      r_cut = idx_topp_cut_exact(w, sm0, sm1, srt, ns, lim, &near);
+      if (__ballot(near)) flags |= TC_FLAG_NEAR_TIE;
+    }
+  }
+  const uint32_t live_r = r_cut > (uint32_t)a.min_keep ? r_cut : (uint32_t)a.min_keep;
+  bool live[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) live[q] = surv[q] && rk[q] < live_r;
+  const uint64_t lm0 = __ballot(live[0]), lm1 = __ballot(live[1]);
+  const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
+  // ---- the draw: softmax over the live scores (f64, + beam score 0.0), inverse CDF
+  double ml = -__builtin_inf();
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+    if (live[q]) ml = ml > (double)sc[q] + 0.0 ? ml : (double)sc[q] + 0.0;
+  ml = dpp_wave_max_d(ml);
+  double e[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) e[q] = live[q] ? tc_exp_d(((double)sc[q] + 0.0) - ml) : 0.0;
+  const double sum2 = dpp_wave_sum_d(e[0] + e[1]);
+  double wv[2];
+  const double rsum2 = 1.0 / sum2;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) wv[q] = live[q] ? e[q] * rsum2 : 0.0;
+  const double acc0 = dpp_scan_f64(wv[0]);
+  const double acc1 = dpp_scan_f64(wv[1]) + rl_f64(acc0, kWave - 1);
+  const double total = rl_f64(acc1, kWave - 1);
+  const double u = reinterpret_cast<const double*>(a.uniforms)[row];
+  const double uu = u * total;
+  const uint64_t pz0 = __ballot(live[0] && wv[0] > 0.0), pz1 = __ballot(live[1] && wv[1] > 0.0);
+  const uint64_t hit0 = __ballot(live[0] && wv[0] > 0.0 && acc0 > uu);
+  const uint64_t hit1 = __ballot(live[1] && wv[1] > 0.0 && acc1 > uu);
+  uint32_t pick;
+  bool found = true;
+  if (hit0) {
+    pick = (uint32_t)__builtin_ctzll(hit0);
+  } else if (hit1) {
+    pick = 64u + (uint32_t)__builtin_ctzll(hit1);
+  } else {
+    found = false;  // the last positive weight
+    pick = pz1 ? 64u + 63u - (uint32_t)__builtin_clzll(pz1) : (pz0 ? 63u - (uint32_t)__builtin_clzll(pz0) : 0u);
+  }
+  {
+    // robustness: the running sums of the pick and of the positive element
+    // before it against uu
+    const double mg = order_margin(nl) * total;
+    const double a_pick = rl_f64(pick < 64 ? acc0 : acc1, (int)(pick & 63u));
+    bool close = __builtin_fabs(a_pick - uu) <= mg;
+    if (found) {
+      const uint64_t below0 = pick < 64 ? (pz0 & ((1ull << pick) - 1ull)) : pz0;
+      const uint64_t below1 = pick < 64 ? 0ull : (pz1 & ((1ull << (pick - 64u)) - 1ull));
+      if (below1 || below0) {
+        const uint32_t prev = below1 ? 64u + 63u - (uint32_t)__builtin_clzll(below1) : 63u - (uint32_t)__builtin_clzll(below0);
+        const double a_prev = rl_f64(prev < 64 ? acc0 : acc1, (int)(prev & 63u));
+        close = close || __builtin_fabs(a_prev - uu) <= mg;
+      }
+    }
+    if (close) {
+      // the reference's order: sequential sums in vocabulary order
+      double s2 = -0.0;
+      for (uint64_t m = lm0; m; m &= m - 1) s2 += rl_f64(e[0], __builtin_ctzll(m));
+      for (uint64_t m = lm1; m; m &= m - 1) s2 += rl_f64(e[1], __builtin_ctzll(m));
+#pragma unroll
+      for (int q = 0; q < 2; ++q) wv[q] = live[q] ? e[q] / s2 : 0.0;
+      double tot = -0.0;
+      for (uint64_t m = lm0; m; m &= m - 1) tot += rl_f64(wv[0], __builtin_ctzll(m));
+      for (uint64_t m = lm1; m; m &= m - 1) tot += rl_f64(wv[1], __builtin_ctzll(m));
+      const double ue = u * tot;
+      double acc = 0.0;
+      uint32_t last = 0xffffffffu, pk = 0xffffffffu;
+      bool near = false;
+      for (int c = 0; c < (int)n && pk == 0xffffffffu; ++c) {
+        const uint64_t lm = c < 64 ? lm0 : lm1;
+        if (!((lm >> (c & 63)) & 1ull)) continue;
+        if (last == 0xffffffffu) last = (uint32_t)c;  // last_positive starts at live[0]
+        const double wc = rl_f64(c < 64 ? wv[0] : wv[1], c & 63);
+        if (wc <= 0.0) continue;
+        last = (uint32_t)c;
+        acc += wc;
+        if (__builtin_fabs(acc - ue) <= exp_margin() * tot) near = true;
+        if (acc > ue) pk = (uint32_t)c;
+      }
+      pick = pk != 0xffffffffu ? pk : last;
+      if (near) flags |= TC_FLAG_NEAR_TIE;
+    }
+  }
+  const uint32_t tok = nl ? rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u)) : 0u;
+  if (lane == 0) {
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = nl ? TC_OK : TC_ETOOFEW;
+    if (a.out_flags) a.out_flags[row] = flags;
+    if (a.topk_count) {
+      a.topk_count[row] = ns;
+      a.keep_count[row] = nl;
+    }
+  }
+  if (a.topk_count) {
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint64_t smq = q == 0 ? sm0 : sm1, lmq = q == 0 ? lm0 : lm1;
+      const uint32_t so = q == 0 ? 0u : (uint32_t)__popcll(sm0), lo = q == 0 ? 0u : (uint32_t)__popcll(lm0);
+      if (surv[q]) {
+        const uint32_t j = so + (uint32_t)__popcll(smq & below);
+        if (j < a.cap) a.topk_ids[(size_t)row * a.cap + j] = id[q];
+      }
+      if (live[q]) {
+        const uint32_t j = lo + (uint32_t)__popcll(lmq & below);
+        if (j < a.cap) {
+          a.keep_ids[(size_t)row * a.cap + j] = id[q];
+          a.keep_probs[(size_t)row * a.cap + j] = (float)wv[q];
+        }
+      }
+    }
+  }
+}
+
+}  // namespace tc

@@ -144,12 +144,14 @@ TC_HD uint32_t tc_toward(double y, float r) {
 }
 
 // Distance of a double y from the float rounding midpoint next to r = (float)y,
-// in units of the float spacing there.  0.5 means y is exactly a float.
+// in units of the float spacing there.  0.5 means y is exactly a float.  The
+// spacing is a power of two, so the quotient is a multiplication by its exact
+// reciprocal.
 TC_HD double tc_mid_dist(double y, float r) {
   uint32_t nbb = tc_toward(y, r);
   float nb;
   memcpy(&nb, &nbb, 4);
   double gap = fabs((double)nb - (double)r);
   double mid = 0.5 * ((double)nb + (double)r);
-  return fabs(y - mid) / gap;
+  return fabs(y - mid) * ldexp(1.0, -ilogb(gap));
 }

@@ -139,9 +139,12 @@ def launch_shape(vocab: int, dtype: int = F32) -> tuple[int, int]:
     """(items per thread, threads per block) the library uses for one row of
     ``vocab`` logits (mirrors pick_shape in csrc/sampler.hip)."""
     pad = 7 if dtype == BF16 else 3
-    for items, max_t in ((8, 1024), (16, 768), (24, 704)):
+    for items in ((8, 16, 24) if dtype == BF16 else (8, 12, 16, 24)):
+        max_t = 1024 if items <= 8 else (768 if items <= 16 else 704)
         nt = -(-(vocab + pad) // items)
         nt = max(256, -(-nt // 64) * 64)
-        if nt <= max_t:
-            return items, nt
+        if nt > max_t:
+            continue
+        bal = -(-nt // 256) * 256
+        return items, (bal if bal <= max_t else nt)
     raise ValueError(f"vocab {vocab} exceeds the register-resident kernel")

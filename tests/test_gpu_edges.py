@@ -87,7 +87,9 @@ def same(g, o, rows=None, probs_exact=True):
             continue
         assert g["status"][r] == 0, (r, g["status"][r])
         assert g["ids"][r] == o["ids"][r], (r, g["ids"][r], o["ids"][r])
-        assert g["flags"][r] == o["flags"][r], (r, g["flags"][r], o["flags"][r])
+        # TC_FLAG_NEAR_TIE (16) reports a decision within the f64 exp error of the
+        # reference's libm; the oracle has no such flag
+        assert g["flags"][r] & ~16 == o["flags"][r], (r, g["flags"][r], o["flags"][r])
         for c, i in (("topk_count", "topk_ids"), ("keep_count", "keep_ids")):
             assert g[c][r] == o[c][r], (r, c, g[c][r], o[c][r])
             n = min(int(g[c][r]), CAP)
