@@ -37,7 +37,25 @@ def parse():
     ap.add_argument("--pool-mb", type=int, default=640, help="rotating input pool (MB of logits)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="after the timed region, copy 256 MiB three times (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
+
+
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the sampler kernel, measured with rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE and scaled by a plain copy of known size (the
+    summary in profiles/traffic_<workload>.txt), or None."""
+    path = os.path.join(PROFILES, f"traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def cpu_baseline(w, batch, seconds: float):
@@ -132,6 +150,12 @@ def main():
     if (st != 0).any():
         print(f"bench.py: {int((st != 0).sum())} rows returned a non-OK status", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calib:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     bytes_per_row = w.algorithmic_bytes_per_row()
     bytes_per_launch = bytes_per_row * w.rows
     achieved = bytes_per_launch / (k_avg_us * 1e-6) / 1e9
@@ -153,7 +177,7 @@ def main():
                    "penalty": w.penalty, "temperature": w.temperature, "top_k": w.top_k, "top_p": w.top_p,
                    "variant": "indextts", "pool_batches": n_pool, "seed": w.seed},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(w.name),
                      "kernel_avg_us": round(k_avg_us, 3), "kernel_median_us": round(k_med_us, 3),
                      "algorithmic_bytes_per_launch": bytes_per_launch},
     }
