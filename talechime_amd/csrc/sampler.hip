@@ -678,56 +678,70 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
         force |= (v && !(d[i] >= -87.0f) ? 1u : 0u) << i;  // below the approximation's range
       }
       if (mns > -16.0f) atomicAdd(&F.bins[(uint32_t)(-mns * 4.0f)], 1u);
-      bool ok = true;
-      float S = block_seqsum_fast<ITEMS>(ap, exm, force, d, [](float v) { return expf_glibc(v); }, e0, F.seq, &ok);
-      if (!ok) {
-        float ex[ITEMS];
-#pragma unroll
-        for (int i = 0; i < ITEMS; ++i) ex[i] = ((vm >> i) & 1u) ? expf_glibc(d[i]) : 0.0f;
-        __syncthreads();
-        S = block_seqsum_slow<ITEMS>(ex, e0, V, F.seq.x, SeqFastLds::kCap, &F.seq.S);
-      }
-      const float L = logf_glibc(S);
-      put_norm(a, row, L);
-      // the bucket of the K-th largest thread maximum (the histogram is complete
-      // after the first barrier in block_seqsum_fast)
+      SeqSum<ITEMS> sq;
+      sq.predict(ap, F.seq);
+      lds_barrier();
+      sq.classify(ap, exm, force, e0, F.seq);
+      // Candidates, staged while the exact sum is finished.  The histogram of
+      // per-thread maxima of d over ids not in the history puts the K-th largest
+      // such d above -(b0 + 1) / 4; x' = d - L is monotone in d for those ids, so
+      // every one whose x' can reach the K-th largest has d >= -(b0 + 1) / 4 less
+      // a margin (2^-9, far above the roundings of d - L and the floats the
+      // division by T can merge).  Ids in the history (x' * pen) are admitted
+      // against the same bound for every L the prediction allows.
       const uint32_t cum = dpp_scan_u32(F.bins[lane_id()]);
       const uint64_t reach = __ballot(cum >= (uint32_t)a.K);
+      uint32_t sel = 0;
       if (reach) {
-        // the K-th largest x' is at least fl(-(b0 + 1) / 4 - L); 2^-10 covers the
-        // roundings of that bound and the floats the division by T merges
         const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
-        const float thr = (-(float)(b0 + 1u) * 0.25f - L) - 0x1p-10f;
-        // x' = (x - max) - L; repetition penalty on the log-probs
-        // (generation.rs:122-134): x' <= 0 here (L = ln S >= 0), where
-        // s < 0 ? s * pen : s / pen equals s * pen, signed zeros included
-        uint64_t key[ITEMS];
-        uint32_t sel = 0;
+        const float thr_d = -(float)(b0 + 1u) * 0.25f - 0x1p-9f;
+        float L_lo = 0.0f, L_hi = 0.0f;
+        if (seen) {
+          const float Sp = sq.total(F.seq), tt = seq_tau(V);
+          L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f;
+          L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
+        }
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i) {
-          float v = d[i] - L;
-          v = ((seen >> i) & 1ull) ? v * a.pen_f : v;
-          key[i] = ((uint64_t)tkey(v) << 32) | (uint32_t)(e0 + i);
-          sel |= ((((vm >> i) & 1u) && v >= thr) ? 1u : 0u) << i;
+          const bool v = (vm >> i) & 1u, sn = (seen >> i) & 1ull;
+          const bool ok = sn ? ((d[i] - L_lo) * a.pen_f >= thr_d - L_hi) : d[i] >= thr_d;
+          sel |= (v && ok ? 1u : 0u) << i;
         }
-        const uint32_t c = (uint32_t)__builtin_popcount(sel);
-        const uint32_t ci = dpp_scan_u32(c);
-        if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
-        lds_barrier();
-        uint32_t off = ci - c, n = 0;
-        for (int w = 0; w < num_waves(); ++w) {
-          const uint32_t cw = F.wcand[w];
-          off += w < wave_id() ? cw : 0u;
-          n += cw;
-        }
-        if (n <= (uint32_t)FinLds::kCap) {
+      }
+      const uint32_t c = (uint32_t)__builtin_popcount(sel);
+      const uint32_t ci = dpp_scan_u32(c);
+      if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
+      lds_barrier();
+      const bool listed_ok = sq.write_list(ap, d, e0, F.seq);
+      uint32_t off = ci - c, n = 0;
+      for (int w = 0; w < num_waves(); ++w) {
+        const uint32_t cw = F.wcand[w];
+        off += w < wave_id() ? cw : 0u;
+        n += cw;
+      }
+      if (reach && n <= (uint32_t)FinLds::kCap) {
 #pragma unroll
-          for (int i = 0; i < ITEMS; ++i)
-            if ((sel >> i) & 1u) F.fin.cand[off++] = key[i];
-          lds_barrier();
-          if (wave_id() == 0) idx_fast_finish(a, row, n, F.fin);
-          return;
+        for (int i = 0; i < ITEMS; ++i)
+          if ((sel >> i) & 1u)
+            F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) |
+                                (uint32_t)(e0 + i);
+        lds_barrier();
+        if (listed_ok && wave_id() == 0) sq.replay([](float v) { return expf_glibc(v); }, F.seq);
+        lds_barrier();
+        float S = F.seq.S;
+        if (!listed_ok || F.seq.bad) {
+          float ex[ITEMS];
+#pragma unroll
+          for (int i = 0; i < ITEMS; ++i) ex[i] = ((vm >> i) & 1u) ? expf_glibc(d[i]) : 0.0f;
+          __syncthreads();
+          S = block_seqsum_slow<ITEMS>(ex, e0, V, F.seq.x, SeqFastLds::kCap, &F.seq.S);
         }
+        if (wave_id() == 0) {
+          const float L = logf_glibc(S);
+          put_norm(a, row, L);
+          idx_fast_finish(a, row, n, L, F.fin);
+        }
+        return;
       }
     }
     __syncthreads();

@@ -40,6 +40,9 @@ __device__ __forceinline__ double dpp_f64(double v) {
 
 __device__ __forceinline__ uint32_t rl_u32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
 __device__ __forceinline__ float rl_f32(float v, int l) { return __uint_as_float(rl_u32(__float_as_uint(v), l)); }
+__device__ __forceinline__ uint64_t rl_u64(uint64_t v, int l) {
+  return ((uint64_t)rl_u32((uint32_t)(v >> 32), l) << 32) | rl_u32((uint32_t)v, l);
+}
 __device__ __forceinline__ double rl_f64(double v, int l) {
   const uint64_t b = (uint64_t)__double_as_longlong(v);
   return __longlong_as_double((long long)(((uint64_t)rl_u32((uint32_t)(b >> 32), l) << 32) | rl_u32((uint32_t)b, l)));

@@ -80,98 +80,145 @@ __device__ __forceinline__ float seq_tau(int pos) {
   return (float)(pos + 64) * 0x1p-24f * 1.01f + kSeqErr + 0x1p-21f;
 }
 
-// The exact term of one element from its input (the caller's functor) with
-// the correctly rounded exp computed in place: f(x) is the reference's term.
-// Thread t holds ITEMS terms at element positions pos0 + i (threads in order,
-// positions increasing).  ap[i]: the term, exact where bit i of `exact_mask`
-// is set (invalid positions: an exact 0), otherwise within kSeqErr of f(x[i]),
-// the exact term; bits of `force` are treated as undecided whatever ap holds.
-// LDS writes the caller issued before the call are complete and visible after
-// its first barrier.  Returns the sum, or sets *ok = false when more than kCap
-// elements need the replay or the replay met an inconsistency (the caller
-// then sums literally).  Every thread of the block must call it.
-template <int ITEMS, class F>
-__device__ __forceinline__ float block_seqsum_fast(const float (&ap)[ITEMS], uint32_t exact_mask, uint32_t force,
-                                                   const float (&x)[ITEMS], F f, int pos0, SeqFastLds& L, bool* ok) {
-  const int lane = lane_id(), wv = wave_id();
-  // 1. prediction: f32 partial sums, exclusive prefix over threads
-  float D = 0.0f;
-#pragma unroll
-  for (int i = 0; i < ITEMS; ++i) D += ap[i];
-  const float inc = dpp_scan_f32(D);
-  const float ex = dpp_prev_f32(inc);  // earlier lanes of this wave
-  if (lane == kWave - 1) L.wsum[wv] = inc;
-  lds_barrier();
-  float off = 0.0f;
-  for (int w = 0; w < wv; ++w) off += L.wsum[w];
-  const float P0 = off + ex;
-  const float tau = seq_tau(pos0 + ITEMS);
-  const float m_lo = 1.0f - tau, m_hi = 1.0f + tau;
-  // 2. classify with the terms at hand; undecided and listed elements go to
-  // the replay list
+// The exact sequential sum in stages, so that a kernel can put its own work
+// on the same barriers:
+//   predict()     f32 partial sums, their wave scan; writes L.wsum
+//   -- barrier --
+//   classify()    the prediction P0 of each thread; grid rounding of every
+//                 element; the list of undecided and listed elements and its
+//                 (count, integer sum) wave scans; writes L.wcnt / L.wq
+//   -- barrier --
+//   write_list()  list offsets; writes the list (false: more than kCap)
+//   -- barrier --
+//   replay()      wave 0: the exact terms of the listed elements in parallel,
+//                 the undecided ones classified again (safe ones fold into
+//                 the integer sums), then one walk over the rest; writes
+//                 L.S / L.bad
+// Thread t holds ITEMS terms at element positions pos0 + i (threads in
+// order, positions increasing).  ap[i]: the term, exact where bit i of
+// exact_mask is set (invalid positions: an exact 0), otherwise within kSeqErr
+// of the exact term f(x[i]); bits of `force` are undecided whatever ap holds.
+template <int ITEMS>
+struct SeqSum {
+  float D, ex;
+  float P0;
   uint32_t r[ITEMS];
-  uint32_t unsafe = 0, amb = force;
-  {
-    float P = P0;
+  uint32_t listed, amb, exact;
+  uint32_t cnt, rsum, ci, qi;
+  uint32_t c_tot, q_tot;
+
+  __device__ __forceinline__ void predict(const float (&ap)[ITEMS], SeqFastLds& L) {
+    D = 0.0f;
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const float Pn = P + ap[i];
-      const uint32_t c = seq_classify(P, Pn, ap[i], (exact_mask >> i) & 1u, m_lo, m_hi, &r[i]);
-      amb |= (c == 1u ? 1u : 0u) << i;
-      unsafe |= (c == 2u ? 1u : 0u) << i;
-      P = Pn;
-    }
+    for (int i = 0; i < ITEMS; ++i) D += ap[i];
+    const float inc = dpp_scan_f32(D);
+    ex = dpp_prev_f32(inc);  // earlier lanes of this wave
+    if (lane_id() == kWave - 1) L.wsum[wave_id()] = inc;
   }
-  amb &= ~unsafe;
-  const uint32_t listed = unsafe | amb;
-  uint32_t rsum = 0;
+
+  // The prediction of the whole sum (valid after the first barrier).
+  __device__ __forceinline__ float total(const SeqFastLds& L) const {
+    float t = 0.0f;
+    for (int w = 0; w < num_waves(); ++w) t += L.wsum[w];
+    return t;
+  }
+
+  __device__ __forceinline__ void classify(const float (&ap)[ITEMS], uint32_t exact_mask, uint32_t force, int pos0,
+                                           SeqFastLds& L) {
+    const int wv = wave_id();
+    float off = 0.0f;
+    for (int w = 0; w < wv; ++w) off += L.wsum[w];
+    P0 = off + ex;
+    exact = exact_mask;
+    const float tau = seq_tau(pos0 + ITEMS);
+    const float m_lo = 1.0f - tau, m_hi = 1.0f + tau;
+    uint32_t unsafe = 0;
+    amb = force;
+    // a thread whose whole range provably stays in one binade rounds every
+    // term on that binade's grid; a wave takes the short form when all of its
+    // threads can (no divergence inside a wave)
+    const uint32_t pb0 = __float_as_uint(P0);
+    const uint32_t eb0 = pb0 & 0x7f800000u;
+    const bool uni = P0 > 0.0f && pb0 >= 0x0b800000u && pb0 < 0x4b000000u && P0 * m_lo >= __uint_as_float(eb0) &&
+                     (P0 + D) * (m_hi + 0x1p-20f) < __uint_as_float(eb0 + 0x00800000u);
+    if (__ballot(!uni) == 0ull) {
+      const float scale = __uint_as_float(0x8a800000u - eb0);  // 2^(23-e)
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) rsum += ((listed >> i) & 1u) ? 0u : r[i];
-  // 3. the list in element order: exclusive scan of (count, rsum)
-  const uint32_t cnt = (uint32_t)__builtin_popcount(listed);
-  const uint32_t ci = dpp_scan_u32(cnt), qi = dpp_scan_u32(rsum);
-  if (lane == kWave - 1) {
-    L.wcnt[wv] = ci;
-    L.wq[wv] = qi;
-  }
-  lds_barrier();
-  uint32_t c_off = ci - cnt, q_off = qi - rsum, c_tot = 0, q_tot = 0;
-  for (int w = 0; w < num_waves(); ++w) {
-    const uint32_t wc = L.wcnt[w], wq = L.wq[w];
-    if (w < wv) {
-      c_off += wc;
-      q_off += wq;
-    }
-    c_tot += wc;
-    q_tot += wq;
-  }
-  if (c_tot > (uint32_t)SeqFastLds::kCap) {
-    *ok = false;
-    return 0.0f;
-  }
-  if (listed) {
-    uint32_t k = c_off, q = q_off;
-    float P = P0;
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      if ((listed >> i) & 1u) {
-        const bool exa = (exact_mask >> i) & 1u;
-        L.x[k] = exa ? ap[i] : x[i];
-        L.P[k] = P;
-        L.q[k] = q;
-        L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | ((uint32_t)(pos0 + i) << 8);
-        ++k;
-      } else {
-        q += r[i];
+      for (int i = 0; i < ITEMS; ++i) {
+        const float q = ap[i] * scale;
+        const float fl = __builtin_floorf(q), fr = q - fl;
+        const bool ex_i = (exact_mask >> i) & 1u;
+        const bool am = !ex_i && __builtin_fabsf(fr - 0.5f) <= q * (2.0f * kSeqErr) + 0x1p-24f;
+        r[i] = (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
+        amb |= (am ? 1u : 0u) << i;
+        unsafe |= (!am && fr == 0.5f ? 1u : 0u) << i;
       }
-      P = P + ap[i];
+    } else {
+      float P = P0;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        const float Pn = P + ap[i];
+        const uint32_t c = seq_classify(P, Pn, ap[i], (exact_mask >> i) & 1u, m_lo, m_hi, &r[i]);
+        amb |= (c == 1u ? 1u : 0u) << i;
+        unsafe |= (c == 2u ? 1u : 0u) << i;
+        P = Pn;
+      }
+    }
+    amb &= ~unsafe;
+    listed = unsafe | amb;
+    rsum = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) rsum += ((listed >> i) & 1u) ? 0u : r[i];
+    cnt = (uint32_t)__builtin_popcount(listed);
+    ci = dpp_scan_u32(cnt);
+    qi = dpp_scan_u32(rsum);
+    if (lane_id() == kWave - 1) {
+      L.wcnt[wv] = ci;
+      L.wq[wv] = qi;
     }
   }
-  lds_barrier();
-  // 4. the replay (wave 0): per chunk of 64 listed elements, the exact terms
-  // in parallel, the undecided ones classified again (those that turn out
-  // safe fold into the integer contributions), then one walk over the rest
-  if (wv == 0) {
+
+  __device__ __forceinline__ bool write_list(const float (&ap)[ITEMS], const float (&x)[ITEMS], int pos0,
+                                             SeqFastLds& L) {
+    const int wv = wave_id();
+    uint32_t c_off = ci - cnt, q_off = qi - rsum;
+    c_tot = 0;
+    q_tot = 0;
+    for (int w = 0; w < num_waves(); ++w) {
+      const uint32_t wc = L.wcnt[w], wq = L.wq[w];
+      if (w < wv) {
+        c_off += wc;
+        q_off += wq;
+      }
+      c_tot += wc;
+      q_tot += wq;
+    }
+    if (c_tot > (uint32_t)SeqFastLds::kCap) return false;
+    if (listed) {
+      uint32_t k = c_off, q = q_off;
+      float P = P0;
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) {
+        if ((listed >> i) & 1u) {
+          const bool exa = (exact >> i) & 1u;
+          L.x[k] = exa ? ap[i] : x[i];
+          L.P[k] = P;
+          L.q[k] = q;
+          L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | ((uint32_t)(pos0 + i) << 8);
+          ++k;
+        } else {
+          q += r[i];
+        }
+        P = P + ap[i];
+      }
+    }
+    return true;
+  }
+
+  // Wave 0 only.
+  template <class F>
+  __device__ __forceinline__ void replay(F f, SeqFastLds& L) const {
+    const int lane = lane_id();
     float s = -0.0f;
     uint32_t qp = 0, bad = 0, fold = 0;
     for (uint32_t base = 0; base < c_tot; base += kWave) {
@@ -212,10 +259,7 @@ __device__ __forceinline__ float block_seqsum_fast(const float (&ap)[ITEMS], uin
       L.bad = bad;
     }
   }
-  lds_barrier();
-  *ok = L.bad == 0u;
-  return L.S;
-}
+};
 
 // ---------------------------------------------------------------- one-wave finish (indextts)
 // Relative distance within which a comparison of two f64 sums of n
@@ -228,122 +272,146 @@ __device__ __forceinline__ double exp_margin() { return 0x1p-46; }
 
 struct FinLds {
   static constexpr int kCap = 128;
-  uint64_t cand[kCap];     // (tkey(x'), id) in vocabulary order
-  uint32_t rank_of[kCap];  // rank (value descending, id descending) of vocabulary-order candidate c
-  double pr[kCap];         // by rank: top-p probability
+  uint64_t cand[kCap];      // (bits of d, history bit 31 | id) in vocabulary order
+  uint64_t rkey[kCap + 4];  // rank keys, zero padded
+  double wr[kCap];          // top-p weights by ascending position (rank ns-1-p)
 };
 
-// The reference's order for an ascending cumulative walk and the draw, one
-// lane walking uniform loops; used when a wave-scan decision is too close to
-// call.
-__device__ __forceinline__ uint32_t idx_topp_cut_exact(const double (&w)[2], uint64_t sm0, uint64_t sm1,
-                                                       const uint64_t (&srt)[2], uint32_t ns, double lim, bool* near) {
-  double sr = -0.0;
-  for (uint64_t m = sm0; m; m &= m - 1) sr += rl_f64(w[0], __builtin_ctzll(m));
-  for (uint64_t m = sm1; m; m &= m - 1) sr += rl_f64(w[1], __builtin_ctzll(m));
-  double cum = 0.0;
-  uint32_t rc = ns;
-  for (int p = (int)ns - 1; p >= 0; --p) {
-    const uint32_t c = (uint32_t)rl_u32((uint32_t)(p < 64 ? srt[0] : srt[1]), p & 63);
-    const double wc = rl_f64(c < 64 ? w[0] : w[1], (int)(c & 63u));
-    cum += wc / sr;
-    if (__builtin_fabs(cum - lim) <= exp_margin() * (cum > lim ? cum : lim)) *near = true;
-    if (cum <= lim) rc = (uint32_t)p;
-  }
-  return rc;
-}
-
 // One-wave finish of an indextts row from its n (K <= n <= 128) candidates
-// (F.cand, vocabulary order; the scores before the division by T): the
-// top-k cut (generation.rs:148-161), top-p (169-194) and one draw of
-// sample_without_replacement (280-303) on x'' = x' / T.  Every element whose
-// score can reach the k-th largest is a candidate; all scores are finite.
-__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, FinLds& F) {
+// (F.cand, vocabulary order, each with d = x - max and whether its id is in
+// the history): x' = d - L, the penalty, x'' = x' / T, the top-k cut
+// (generation.rs:148-161), top-p (169-194) and one draw of
+// sample_without_replacement (280-303).  Every element whose score can reach
+// the k-th largest is a candidate; all scores are finite.
+//
+// Ranks are counted against every candidate's key, broadcast from LDS.  The
+// f64 weights exp(x'' - max) serve both top-p and the draw (their maxima
+// coincide: the top score is never removed while min_keep >= 1, and with
+// min_keep = 0 the walk keeps it too unless top_p <= 0, where the row has no
+// live entry and the reference fails the same way).  The cumulative tests
+// compare unnormalised tree sums against lim * sum and u * sum2;
+// order_margin bounds everything that separates them from the reference's
+// sequential, normalised sums, and the reference's loops run whenever a
+// decision falls inside it.
+__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
   const int lane = lane_id();
   float sc[2];
   uint32_t id[2];
   bool has[2];
-  uint64_t srt[2];
+  uint64_t key[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const uint32_t c = (uint32_t)(q * kWave + lane);
     has[q] = c < n;
     const uint64_t v = has[q] ? F.cand[c] : 0ull;
-    id[q] = (uint32_t)v;
-    const float xp = untkey((uint32_t)(v >> 32));
+    id[q] = (uint32_t)v & 0x7fffffffu;
+    // log_softmax, then the penalty on the log-prob (x' <= 0: s * pen), then T
+    float xp = u2f((uint32_t)(v >> 32)) - L;
+    xp = ((uint32_t)v & 0x80000000u) ? xp * a.pen_f : xp;
     sc[q] = a.do_temp ? xp / a.t_f : xp;
-    // rank key: value descending, then the later id first (the reverse of the
-    // reference's ascending stable order)
-    srt[q] = has[q] ? (((uint64_t)tkey(sc[q]) << 32) | c) : 0ull;
+    // rank order: value descending, then the later id first (the reverse of
+    // the reference's ascending stable order)
+    key[q] = has[q] ? (((uint64_t)tkey(sc[q]) << 32) | c) : 0ull;
+    if (has[q]) F.rkey[c] = key[q];
   }
-  if (n <= (uint32_t)kWave) {
-    uint64_t one[1] = {srt[0]};
-    dpp_sort_desc_u64<1>(one);
-    srt[0] = one[0];
-    srt[1] = 0ull;
-  } else {
-    dpp_sort_desc_u64<2>(srt);
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint32_t p = (uint32_t)(q * kWave + lane);
-    if (p < n) F.rank_of[(uint32_t)srt[q]] = p;
-  }
+  if (lane < 4) F.rkey[n + (uint32_t)lane] = 0ull;
   lds_wait();
-  uint32_t rk[2];
-#pragma unroll
-  for (int q = 0; q < 2; ++q) rk[q] = has[q] ? F.rank_of[q * kWave + lane] : 0xffffffffu;
+  // rank = number of candidates with a larger key
+  uint32_t rk0 = 0, rk1 = 0;
+  {
+    const uint32_t nr = (n + 3u) & ~3u;
+    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+    if (n <= (uint32_t)kWave) {
+      for (uint32_t j = 0; j < nr; j += 4) {
+        a0 += F.rkey[j] > key[0] ? 1u : 0u;
+        a1 += F.rkey[j + 1] > key[0] ? 1u : 0u;
+        a2 += F.rkey[j + 2] > key[0] ? 1u : 0u;
+        a3 += F.rkey[j + 3] > key[0] ? 1u : 0u;
+      }
+      rk0 = (a0 + a1) + (a2 + a3);
+    } else {
+      uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+      for (uint32_t j = 0; j < nr; j += 4) {
+        const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1], k2 = F.rkey[j + 2], k3 = F.rkey[j + 3];
+        a0 += k0 > key[0] ? 1u : 0u;
+        a1 += k1 > key[0] ? 1u : 0u;
+        a2 += k2 > key[0] ? 1u : 0u;
+        a3 += k3 > key[0] ? 1u : 0u;
+        b0 += k0 > key[1] ? 1u : 0u;
+        b1 += k1 > key[1] ? 1u : 0u;
+        b2 += k2 > key[1] ? 1u : 0u;
+        b3 += k3 > key[1] ? 1u : 0u;
+      }
+      rk0 = (a0 + a1) + (a2 + a3);
+      rk1 = (b0 + b1) + (b2 + b3);
+    }
+  }
+  const uint32_t rk[2] = {has[0] ? rk0 : 0xffffffffu, has[1] ? rk1 : 0xffffffffu};
   const uint32_t K = (uint32_t)a.K;
-  const float kth = untkey(rl_u32((uint32_t)((K - 1) < 64 ? srt[0] >> 32 : srt[1] >> 32), (int)((K - 1) & 63)));
-  const float vmax = untkey(rl_u32((uint32_t)(srt[0] >> 32), 0));
+  const uint64_t bk0 = __ballot(rk[0] == K - 1), bk1 = __ballot(rk[1] == K - 1);
+  const float kth = bk0 ? rl_f32(sc[0], __builtin_ctzll(bk0)) : (bk1 ? rl_f32(sc[1], __builtin_ctzll(bk1)) : -__builtin_inff());
+  const uint64_t bm0 = __ballot(rk[0] == 0u), bm1 = __ballot(rk[1] == 0u);
+  const float vmax = bm0 ? rl_f32(sc[0], __builtin_ctzll(bm0)) : rl_f32(sc[1], __builtin_ctzll(bm1));
   bool surv[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) surv[q] = has[q] && !(sc[q] < kth);
   const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
   const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  // f64 weights (generation.rs:108-116 for top-p, 289-293 for the draw)
+  const double mxd = (double)vmax;
+  double w[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
   uint32_t flags = 0;
   // ---- top-p: ranks [r_cut, ns) are removed, except the min_keep first
   uint32_t r_cut = ns;
   if (a.do_topp) {
-    const double mxd = (double)vmax;
-    double w[2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
     const double sum = dpp_wave_sum_d(w[0] + w[1]);
-    const double rsum = 1.0 / sum;  // within the margin: a product with the reciprocal
 #pragma unroll
     for (int q = 0; q < 2; ++q)
-      if (surv[q]) F.pr[rk[q]] = w[q] * rsum;
+      if (surv[q]) F.wr[ns - 1u - rk[q]] = w[q];
     lds_wait();
-    // ascending position a = rank ns-1-a; cum(a) is the reference's running sum
-    // after adding position a
-    double pa[2];
+    double wa[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t ap = (uint32_t)(q * kWave + lane);
-      pa[q] = ap < ns ? F.pr[ns - 1u - ap] : 0.0;
+      wa[q] = ap < ns ? F.wr[ap] : 0.0;
     }
-    const double c0 = dpp_scan_f64(pa[0]);
-    const double c1 = dpp_scan_f64(pa[1]) + rl_f64(c0, kWave - 1);
+    // cum(position) / sum is the reference's running sum after adding it
+    const double c0 = dpp_scan_f64(wa[0]);
+    const double c1 = dpp_scan_f64(wa[1]) + rl_f64(c0, kWave - 1);
     const double lim = 1.0 - a.top_p_d;
-    const uint64_t rm0 = __ballot((uint32_t)lane < ns && c0 <= lim);
-    const uint64_t rm1 = __ballot((uint32_t)(kWave + lane) < ns && c1 <= lim);
+    const double limS = lim * sum;
+    const uint64_t rm0 = __ballot((uint32_t)lane < ns && c0 <= limS);
+    const uint64_t rm1 = __ballot((uint32_t)(kWave + lane) < ns && c1 <= limS);
     const uint32_t n_rm = (uint32_t)(__popcll(rm0) + __popcll(rm1));
     r_cut = ns - n_rm;
     // the decisions at the last removed and the first kept positions
-    const double mg = order_margin(ns);
+    const double mg = order_margin(ns) * sum;
     bool close = false;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const uint32_t ap = (uint32_t)(q * kWave + lane);
       const double cq = q == 0 ? c0 : c1;
-      if (ap < ns && (ap + 1u == n_rm || ap == n_rm) && __builtin_fabs(cq - lim) <= mg * (cq > lim ? cq : lim))
-        close = true;
+      close = close || (ap < ns && (ap + 1u == n_rm || ap == n_rm) && __builtin_fabs(cq - limS) <= mg);
     }
     if (__ballot(close)) {
+      // the reference's order: the sum in vocabulary order, then the ascending walk
+      double sr = -0.0;
+      for (uint64_t m = sm0; m; m &= m - 1) sr += rl_f64(w[0], __builtin_ctzll(m));
+      for (uint64_t m = sm1; m; m &= m - 1) sr += rl_f64(w[1], __builtin_ctzll(m));
+      double cum = 0.0;
+      uint32_t rc = ns;
       bool near = false;
-      r_cut = idx_topp_cut_exact(w, sm0, sm1, srt, ns, lim, &near);
-      if (__ballot(near)) flags |= TC_FLAG_NEAR_TIE;
+      for (int p = (int)ns - 1; p >= 0; --p) {
+        const uint64_t b0 = __ballot(surv[0] && rk[0] == (uint32_t)p), b1 = __ballot(surv[1] && rk[1] == (uint32_t)p);
+        const double wc = b0 ? rl_f64(w[0], __builtin_ctzll(b0)) : rl_f64(w[1], __builtin_ctzll(b1));
+        cum += wc / sr;
+        near = near || __builtin_fabs(cum - lim) <= exp_margin() * (cum > lim ? cum : lim);
+        if (cum <= lim) rc = (uint32_t)p;
+      }
+      r_cut = rc;
+      if (near) flags |= TC_FLAG_NEAR_TIE;
     }
   }
   const uint32_t live_r = r_cut > (uint32_t)a.min_keep ? r_cut : (uint32_t)a.min_keep;
@@ -352,28 +420,18 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
   for (int q = 0; q < 2; ++q) live[q] = surv[q] && rk[q] < live_r;
   const uint64_t lm0 = __ballot(live[0]), lm1 = __ballot(live[1]);
   const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
-  // ---- the draw: softmax over the live scores (f64, + beam score 0.0), inverse CDF
-  double ml = -__builtin_inf();
-#pragma unroll
-  for (int q = 0; q < 2; ++q)
-    if (live[q]) ml = ml > (double)sc[q] + 0.0 ? ml : (double)sc[q] + 0.0;
-  ml = dpp_wave_max_d(ml);
+  // ---- the draw: exp(x'' + 0.0 - max over live) = w (rank 0 is live), inverse CDF
   double e[2];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) e[q] = live[q] ? tc_exp_d(((double)sc[q] + 0.0) - ml) : 0.0;
-  const double sum2 = dpp_wave_sum_d(e[0] + e[1]);
-  double wv[2];
-  const double rsum2 = 1.0 / sum2;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) wv[q] = live[q] ? e[q] * rsum2 : 0.0;
-  const double acc0 = dpp_scan_f64(wv[0]);
-  const double acc1 = dpp_scan_f64(wv[1]) + rl_f64(acc0, kWave - 1);
-  const double total = rl_f64(acc1, kWave - 1);
+  for (int q = 0; q < 2; ++q) e[q] = live[q] ? w[q] : 0.0;
+  const double acc0 = dpp_scan_f64(e[0]);
+  const double acc1 = dpp_scan_f64(e[1]) + rl_f64(acc0, kWave - 1);
+  const double sum2 = rl_f64(acc1, kWave - 1);
   const double u = reinterpret_cast<const double*>(a.uniforms)[row];
-  const double uu = u * total;
-  const uint64_t pz0 = __ballot(live[0] && wv[0] > 0.0), pz1 = __ballot(live[1] && wv[1] > 0.0);
-  const uint64_t hit0 = __ballot(live[0] && wv[0] > 0.0 && acc0 > uu);
-  const uint64_t hit1 = __ballot(live[1] && wv[1] > 0.0 && acc1 > uu);
+  const double target = u * sum2;
+  const uint64_t pz0 = __ballot(live[0] && e[0] > 0.0), pz1 = __ballot(live[1] && e[1] > 0.0);
+  const uint64_t hit0 = __ballot(live[0] && e[0] > 0.0 && acc0 > target);
+  const uint64_t hit1 = __ballot(live[1] && e[1] > 0.0 && acc1 > target);
   uint32_t pick;
   bool found = true;
   if (hit0) {
@@ -386,17 +444,17 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
   }
   {
     // robustness: the running sums of the pick and of the positive element
-    // before it against uu
-    const double mg = order_margin(nl) * total;
+    // before it against the target
+    const double mg = order_margin(nl) * sum2;
     const double a_pick = rl_f64(pick < 64 ? acc0 : acc1, (int)(pick & 63u));
-    bool close = __builtin_fabs(a_pick - uu) <= mg;
+    bool close = __builtin_fabs(a_pick - target) <= mg;
     if (found) {
       const uint64_t below0 = pick < 64 ? (pz0 & ((1ull << pick) - 1ull)) : pz0;
       const uint64_t below1 = pick < 64 ? 0ull : (pz1 & ((1ull << (pick - 64u)) - 1ull));
       if (below1 || below0) {
         const uint32_t prev = below1 ? 64u + 63u - (uint32_t)__builtin_clzll(below1) : 63u - (uint32_t)__builtin_clzll(below0);
         const double a_prev = rl_f64(prev < 64 ? acc0 : acc1, (int)(prev & 63u));
-        close = close || __builtin_fabs(a_prev - uu) <= mg;
+        close = close || __builtin_fabs(a_prev - target) <= mg;
       }
     }
     if (close) {
@@ -404,6 +462,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
       double s2 = -0.0;
       for (uint64_t m = lm0; m; m &= m - 1) s2 += rl_f64(e[0], __builtin_ctzll(m));
       for (uint64_t m = lm1; m; m &= m - 1) s2 += rl_f64(e[1], __builtin_ctzll(m));
+      double wv[2];
 #pragma unroll
       for (int q = 0; q < 2; ++q) wv[q] = live[q] ? e[q] / s2 : 0.0;
       double tot = -0.0;
@@ -421,7 +480,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
         if (wc <= 0.0) continue;
         last = (uint32_t)c;
         acc += wc;
-        if (__builtin_fabs(acc - ue) <= exp_margin() * tot) near = true;
+        near = near || __builtin_fabs(acc - ue) <= exp_margin() * tot;
         if (acc > ue) pk = (uint32_t)c;
       }
       pick = pk != 0xffffffffu ? pk : last;
@@ -452,7 +511,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
         const uint32_t j = lo + (uint32_t)__popcll(lmq & below);
         if (j < a.cap) {
           a.keep_ids[(size_t)row * a.cap + j] = id[q];
-          a.keep_probs[(size_t)row * a.cap + j] = (float)wv[q];
+          a.keep_probs[(size_t)row * a.cap + j] = (float)(e[q] / sum2);
         }
       }
     }
