@@ -749,6 +749,360 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
   idx_general<InT, ITEMS>(a, U.g);
 }
 
+// ================================================================ qwen, large vocabulary
+// qwen semantics (sampling.rs:169-328 with the per-row penalty of 334-395) for
+// bf16 rows of up to kLargeVocab logits, one 1024-thread workgroup per row.
+// The row streams through in 16-byte chunks (coalesced, one chunk per thread
+// per step) three times; the later passes are served by the caches.
+//  * Pass A: finiteness, the greedy argmax, and the largest bf16 key over ids
+//    outside the history.  Those ids keep the order of their raw keys (the
+//    transform multiplies by positive constants and distinct bf16 values
+//    cannot meet in f32).
+//  * Pass B: an exact histogram of the 256 keys at and below the largest,
+//    which gives the K-th largest such key: a lower bound on the k-th logit.
+//  * Pass C: candidates (ids outside the history at or above that key, ids in
+//    it whose penalised logit reaches the bound; at most kLargeCand), staged
+//    in vocabulary order a tile at a time.
+//  * A bitonic sort gives the reference's rank order (value descending, id
+//    ascending); top-k keeps every value >= the k-th (ties kept).
+//  * top-p: exact terms, the reference's sequential f32 sum in rank order and
+//    its running sum (block_seqsum, seq_prefix), the first crossing kept.
+//  * softmax and the CDF in vocabulary order over the kept ids, again as the
+//    reference's sequential sums; the first index whose running sum reaches u.
+constexpr int kLargeThreads = 1024;
+constexpr int kLargeCand = 2048;
+constexpr int kLargePer = kLargeCand / kLargeThreads;  // candidate slots per thread
+constexpr int kLargeVocab = 262144;
+constexpr int kLargeWords = kLargeVocab / 32;
+
+struct QLargeLds {
+  uint32_t bits[kLargeWords];  // history ids and the EOS id
+  uint32_t hist[256];
+  uint64_t cand[kLargeCand];   // rank order after the sort
+  uint64_t candv[kLargeCand];  // vocabulary order
+  float stage[kLargeCand];
+  uint32_t wtot[2][kMaxWaves];
+  SeqLds sq;
+  ScanLds sc;
+  BlockScratch s;
+  uint32_t misc[8];
+};
+
+// The reference's sequential sum of kLargeCand terms held kLargePer per thread
+// (positions kLargePer * t + q) and its inclusive running sums.
+__device__ __forceinline__ float small_seq_prefix(const float (&tm)[kLargePer], float (&pre)[kLargePer], QLargeLds& S) {
+  SeqThread<kLargePer> th;
+  float t2[kLargePer];
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) t2[q] = tm[q];
+  auto same = [](float v) { return v; };
+  float tot;
+  if (block_seqsum<kLargePer>(t2, ~0u, t2, same, kLargePer * (int)threadIdx.x, 0, th, S.sq, S.sc, &tot)) {
+    seq_prefix<kLargePer>(th, S.sq, pre);
+    return tot;
+  }
+  // one lane walks the staged terms
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) S.stage[kLargePer * threadIdx.x + q] = tm[q];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = -0.0f;
+    for (int p = 0; p < kLargeCand; ++p) {
+      s = s + S.stage[p];
+      S.stage[p] = s;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) pre[q] = S.stage[kLargePer * threadIdx.x + q];
+  tot = S.stage[kLargeCand - 1];
+  __syncthreads();
+  return tot;
+}
+
+// Bits [p, p + 32) of an LDS bitmap of nwords words (p may be negative; bits
+// outside the map read 0).
+__device__ __forceinline__ uint32_t bits_at_fn(const uint32_t* bm, int nwords, int p) {
+  const int w = p >> 5, sh = p & 31;
+  const uint32_t lo = (w >= 0 && w < nwords) ? bm[w] : 0u;
+  const uint32_t hi = (w + 1 >= 0 && w + 1 < nwords) ? bm[w + 1] : 0u;
+  return sh ? ((lo >> sh) | (hi << (32 - sh))) : lo;
+}
+
+// One 16-byte chunk of a bf16 row: the 8 logits of elements q*8 - shift + h
+// as f32 (elements outside [0, V): the most negative finite value), their
+// history/EOS bits, and whether a logit inside the row is non-finite.
+struct LChunk {
+  float x[8];
+  uint32_t sn;  // bit h: in the history or the EOS id
+  bool bad;
+};
+__device__ __forceinline__ LChunk load_lchunk(const uint4* base, int q, int shift, int V, const uint32_t* bits,
+                                              int nwords, int eos) {
+  LChunk c;
+  const int e0 = q * 8 - shift;
+  const uint4 v = base[q];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t hb = bits_at_fn(bits, nwords, e0);
+  c.bad = false;
+  c.sn = 0;
+#pragma unroll
+  for (int h = 0; h < 8; ++h) {
+    const int e = e0 + h;
+    const bool in = e >= 0 && e < V;
+    const uint32_t b = (h & 1) ? (w[h >> 1] & 0xffff0000u) : (w[h >> 1] << 16);
+    c.bad |= in && (b & 0x7f800000u) == 0x7f800000u;
+    c.x[h] = in ? __uint_as_float(b) : -3.3895313892515355e38f;
+    const bool s = ((hb >> h) & 1u) != 0u || e == eos;
+    c.sn |= (s ? 1u : 0u) << h;
+  }
+  return c;
+}
+
+__global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
+  __shared__ QLargeLds S;
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const uint16_t* rp = reinterpret_cast<const uint16_t*>(a.logits) + (size_t)row * (size_t)a.ld;
+  const int shift = (int)((reinterpret_cast<uintptr_t>(rp) >> 1) & 7u);
+  const uint4* base = reinterpret_cast<const uint4*>(rp - shift);
+  const int nchunks = (V + shift + 7) >> 3;
+  const int eos = (a.eos_id >= 0 && a.eos_id < V) ? a.eos_id : -1;
+  // history bitmap
+  const int nwords = (V + 31) >> 5;
+  for (int w = t; w < nwords; w += blockDim.x) S.bits[w] = 0u;
+  if (t < 256) S.hist[t] = 0u;
+  __syncthreads();
+  if (a.do_pen) {
+    uint32_t h0, h1;
+    hist_range(a, row, &h0, &h1);
+    for (uint32_t k = h0 + (uint32_t)t; k < h1; k += blockDim.x) {
+      const uint32_t id = a.hist_ids[k];
+      if (id < (uint32_t)V) atomicOr(&S.bits[id >> 5], 1u << (id & 31u));
+    }
+  }
+  __syncthreads();
+  // the reference's logit after the caller chain and temperature
+  // (synthesis.rs:1238-1276, sampling.rs:175-184)
+  auto logit = [&](float x, bool sn, int e) {
+    float v = x;
+    if (a.do_pen && sn && e != eos) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
+    if (e == eos) v = -__builtin_inff();
+    if (a.do_temp) v = v * a.tmul + 0.0f;
+    return v;
+  };
+  // pass A
+  uint32_t bad = 0, kmax = 0;
+  uint64_t best = 0;
+  for (int q = t; q < nchunks; q += blockDim.x) {
+    const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
+    bad |= c.bad ? 1u : 0u;
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const int e = q * 8 - shift + h;
+      if (a.greedy) {
+        const uint64_t k = ((uint64_t)ckey(logit(c.x[h], (c.sn >> h) & 1u, e)) << 32) | (uint64_t)(~(uint32_t)e);
+        best = (e >= 0 && e < V && k > best) ? k : best;
+      }
+      const uint32_t k16 = ckey(c.x[h]) >> 16;
+      kmax = (!((c.sn >> h) & 1u) && k16 > kmax) ? k16 : kmax;
+    }
+  }
+  bad = block_or_u(bad, S.s);
+  if (bad) {  // NaN / inf: the reference's top-k takes its NaN path; not handled at this vocabulary
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  if (a.greedy) {  // candle argmax: first index whose value is strictly greater
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    if (lane_id() == 0) S.cand[wave_id()] = best;
+    __syncthreads();
+    if (t == 0) {
+      uint64_t b = 0;
+      for (int w = 0; w < num_waves(); ++w) b = S.cand[w] > b ? S.cand[w] : b;
+      finish_row(a, row, b ? ~(uint32_t)(b & 0xffffffffu) : 0u, TC_OK, TC_FLAG_GREEDY);
+    }
+    no_verify(a, row);
+    return;
+  }
+  kmax = block_max_u(kmax, S.s);
+  // pass B: exact histogram of the 256 keys at and below the largest
+  for (int q = t; q < nchunks; q += blockDim.x) {
+    const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+      const uint32_t dk = kmax - (ckey(c.x[h]) >> 16);
+      if (!((c.sn >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
+    }
+  }
+  __syncthreads();
+  const uint32_t K = (uint32_t)a.K;
+  if (wave_id() == 0) {
+    const int l = lane_id();
+    const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
+    const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
+    uint32_t b = 0xffffffffu;
+    if (ex + h0 >= K) b = 4 * l;
+    else if (ex + h0 + h1 >= K) b = 4 * l + 1;
+    else if (ex + h0 + h1 + h2 >= K) b = 4 * l + 2;
+    else if (inc >= K) b = 4 * l + 3;
+    const uint64_t m = __ballot(b != 0xffffffffu && ex < K);
+    if (l == 0) S.misc[0] = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;
+  }
+  __syncthreads();
+  const uint32_t bK = S.misc[0];
+  if (bK == 0xffffffffu) {  // the K-th largest lies more than 256 keys below the largest
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  const uint32_t keyK = kmax - bK;
+  const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
+  const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
+  // pass C: candidates in vocabulary order, a tile of blockDim chunks at a time
+  uint32_t n_c = 0;
+  int parity = 0;
+  for (int tb = 0; tb < nchunks; tb += blockDim.x, parity ^= 1) {
+    const int q = tb + t;
+    uint32_t sel = 0;
+    float v[8];
+    if (q < nchunks) {
+      const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const int e = q * 8 - shift + h;
+        const bool sn = (c.sn >> h) & 1u;
+        v[h] = logit(c.x[h], sn, e);
+        const bool ok = e >= 0 && e < V && (sn ? v[h] >= thr : (ckey(c.x[h]) >> 16) >= keyK);
+        sel |= (ok ? 1u : 0u) << h;
+      }
+    }
+    const uint32_t cnt = (uint32_t)__builtin_popcount(sel);
+    const uint32_t ci = dpp_scan_u32(cnt);
+    if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
+    __syncthreads();
+    uint32_t off = n_c + ci - cnt, tile = 0;
+    for (int w = 0; w < num_waves(); ++w) {
+      const uint32_t tw = S.wtot[parity][w];
+      off += w < wave_id() ? tw : 0u;
+      tile += tw;
+    }
+    if (sel && n_c + tile <= (uint32_t)kLargeCand) {
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+        if ((sel >> h) & 1u) {
+          const uint64_t kv = ((uint64_t)(~ckey(v[h])) << 32) | (uint32_t)(q * 8 - shift + h);
+          S.cand[off] = kv;
+          S.candv[off] = kv;
+          ++off;
+        }
+    }
+    n_c += tile;
+  }
+  __syncthreads();
+  if (n_c > (uint32_t)kLargeCand) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    no_verify(a, row);
+    return;
+  }
+  const int n_pad = next_pow2((int)n_c < 2 ? 2 : (int)n_c);
+  for (int j = (int)n_c + t; j < n_pad; j += blockDim.x) S.cand[j] = ~0ull;
+  __syncthreads();
+  block_bitonic_sort(S.cand, n_pad);
+  // top-k (sampling.rs:224-249): every value >= the K-th largest
+  const uint32_t kth_hi = (uint32_t)(S.cand[K - 1] >> 32);  // ~ckey of the K-th value
+  auto val_of = [](uint64_t kv) { return untkey(~(uint32_t)(kv >> 32)); };
+  uint32_t ns_part = 0;
+  for (int j = t; j < (int)n_c; j += blockDim.x) ns_part += (uint32_t)(S.cand[j] >> 32) <= kth_hi ? 1u : 0u;
+  const uint32_t ns = block_sum_u(ns_part, S.s);
+  const float vmax = val_of(S.cand[0]);
+  uint32_t flags = 0, cut = ns;
+  if (a.do_topp) {
+    // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential
+    // sum, running sum of e / S, cutoff at the first crossing (kept)
+    float e[kLargePer], pre[kLargePer];
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t r = kLargePer * t + q;
+      e[q] = r < ns ? expf_glibc(val_of(S.cand[r]) - vmax) : 0.0f;
+    }
+    float Sr = small_seq_prefix(e, pre, S);
+    float pq[kLargePer];
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) pq[q] = (kLargePer * t + q) < ns ? e[q] / Sr : 0.0f;
+    small_seq_prefix(pq, pre, S);
+    uint32_t first = 0xffffffffu;
+#pragma unroll
+    for (int q = kLargePer - 1; q >= 0; --q)
+      if ((kLargePer * t + q) < ns && pre[q] > a.top_p_f) first = kLargePer * t + q;
+    first = block_min_u(first, S.s);
+    if (first != 0xffffffffu) cut = first + 1;
+    if (cut < ns && (uint32_t)(S.cand[cut - 1] >> 32) == (uint32_t)(S.cand[cut] >> 32)) flags |= TC_FLAG_TIE_CUT;
+  }
+  const uint64_t last_kept = S.cand[cut - 1];
+  // softmax + multinomial in vocabulary order over the kept ids (sampling.rs:302-328)
+  float ev[kLargePer], pre2[kLargePer];
+  bool kept[kLargePer];
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) {
+    const uint32_t j = kLargePer * t + q;
+    kept[q] = j < n_c && S.candv[j] <= last_kept;
+    ev[q] = kept[q] ? expf_glibc(val_of(S.candv[j]) - vmax) : 0.0f;
+  }
+  const float S2 = small_seq_prefix(ev, pre2, S);
+  float pv[kLargePer];
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) pv[q] = kept[q] ? ev[q] / S2 : 0.0f;
+  small_seq_prefix(pv, pre2, S);
+  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+  uint32_t first = 0xffffffffu;
+  if (u > 0.0f) {
+#pragma unroll
+    for (int q = kLargePer - 1; q >= 0; --q)
+      if (kept[q] && pre2[q] >= u) first = kLargePer * t + q;
+  }
+  first = block_min_u(first, S.s);
+  const uint32_t tok = (u > 0.0f && first != 0xffffffffu) ? (uint32_t)S.candv[first] : 0u;
+  finish_row(a, row, tok, TC_OK, flags);
+  put_norm(a, row, S2);
+  if (a.topk_count) {
+    // survivors and kept ids in vocabulary order
+    uint32_t cs = 0, ck = 0;
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t j = kLargePer * t + q;
+      cs += (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) ? 1u : 0u;
+      ck += kept[q] ? 1u : 0u;
+    }
+    uint32_t ts, tk;
+    uint32_t os = block_excl_scan(cs, S.s, &ts);
+    uint32_t ok = block_excl_scan(ck, S.s, &tk);
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t j = kLargePer * t + q;
+      if (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) {
+        if (os < a.cap) a.topk_ids[(size_t)row * a.cap + os] = (uint32_t)S.candv[j];
+        ++os;
+      }
+      if (kept[q]) {
+        if (ok < a.cap) {
+          a.keep_ids[(size_t)row * a.cap + ok] = (uint32_t)S.candv[j];
+          a.keep_probs[(size_t)row * a.cap + ok] = pv[q];
+        }
+        ++ok;
+      }
+    }
+    if (t == 0) {
+      a.topk_count[row] = ts;
+      a.keep_count[row] = tk;
+    }
+  }
+}
+
 // ================================================================ cosyvoice3
 // The softmax denominator and the fallback CDF are the reference's sequential
 // f32 sums, reproduced bit for bit by block_seqsum; the nucleus candidates are
@@ -1484,10 +1838,20 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
     default:
       return fail(TC_EINVAL, "tc_sample: variant %d", p->variant);
   }
-  int items = 0, threads = 0;
-  if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg)
-    return fail(TC_EUNSUPPORTED, "tc_sample: vocab %d exceeds the register-resident kernel", V);
   if ((size_t)V > ctx->max_vocab) return fail(TC_EINVAL, "tc_sample: vocab %d > context max %zu", V, ctx->max_vocab);
+  int items = 0, threads = 0;
+  if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg) {
+    // qwen over bf16 rows up to kLargeVocab: the large-vocabulary kernel
+    if (p->variant == TC_QWEN && dtype == TC_BF16 && V <= tc::kLargeVocab && p->hist_mode != TC_HIST_MASK &&
+        !p->d_add_mask && (a.K >= 1 || a.greedy) && a.K <= tc::kLargeCand) {
+      DeviceGuard g(ctx->device);
+      hipLaunchKernelGGL(tc::k_qwen_large, dim3((unsigned)rows), dim3(tc::kLargeThreads), 0,
+                         reinterpret_cast<hipStream_t>(stream), a);
+      hipError_t e = hipGetLastError();
+      return e == hipSuccess ? TC_OK : hip_fail(e, "tc_sample launch");
+    }
+    return fail(TC_EUNSUPPORTED, "tc_sample: vocab %d exceeds the register-resident kernel", V);
+  }
   DeviceGuard g(ctx->device);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;

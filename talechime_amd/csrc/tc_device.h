@@ -221,6 +221,20 @@ __device__ __forceinline__ uint32_t block_min_u(uint32_t v, BlockScratch& s) {
   return r;
 }
 
+__device__ __forceinline__ uint32_t block_max_u(uint32_t v, BlockScratch& s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t w = __shfl_xor(v, o);
+    v = w > v ? w : v;
+  }
+  if (lane_id() == 0) s.u[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = 0u;
+  for (int w = 0; w < num_waves(); ++w) r = s.u[w] > r ? s.u[w] : r;
+  __syncthreads();
+  return r;
+}
+
 // The K elements that come first under (key descending, element position
 // ascending), given kk = the K-th largest key: every key above kk, then the
 // keys equal to kk in element order until K are taken.  Returns the mask of

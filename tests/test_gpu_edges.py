@@ -409,3 +409,43 @@ def test_indextts_exact_sum_adversarial(sampler):
         big = o["topk_count"] > KSURV
         assert (g["status"][big] == _lib.TC_EUNSUPPORTED).all()
         same(g, o, rows=np.nonzero(~big)[0], probs_exact=False)
+
+
+# ------------------------------------------------------------------ qwen, large vocabulary (bf16)
+@pytest.mark.parametrize("V", [16500, 50001, 151936, 262144])
+def test_qwen_large_vocab_shapes(sampler, V):
+    g_ = np.random.default_rng(V)
+    rows = 4
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    hist = [g_.integers(0, V, 300).tolist() for _ in range(rows)]
+    u = g_.random(rows)
+    for ld_pad, kw in ((0, dict(temperature=0.7, top_k=1000, top_p=0.95, penalty=1.1)),
+                       (3, dict(temperature=1.0, top_k=50, top_p=0.8, penalty=1.05, eos_id=7)),
+                       (5, dict(temperature=0.9, top_k=2000, top_p=1.0, penalty=1.0))):
+        g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, ld_pad=ld_pad, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+def test_qwen_large_vocab_greedy_broadcast_and_unsupported(sampler):
+    g_ = np.random.default_rng(5)
+    V = 151936
+    x = (g_.standard_normal((3, V)) * 3).astype(np.float32)
+    x[1, 100:104] = x[1].max() + 1.0  # ties at the top: the first index wins
+    g, o = run(sampler, O.QWEN, x, [[1, 2, 3]], [0.3, 0.6, 0.9], bf16=True, hist_mode=1, temperature=0.005,
+               top_k=50, top_p=0.9, penalty=1.2)
+    assert (g["status"] == 0).all()
+    assert g["ids"].tolist() == o["ids"].tolist()
+    assert (g["flags"] == _lib.FLAG_GREEDY).all()
+    # broadcast history, sampled
+    g, o = run(sampler, O.QWEN, x, [[int(v) for v in g_.integers(0, V, 500)]], [0.3, 0.6, 0.9], bf16=True,
+               hist_mode=1, temperature=0.8, top_k=300, top_p=0.9, penalty=1.3)
+    assert (g["status"] == 0).all()
+    tie = (o["flags"] & 1) != 0
+    same(g, o, rows=[r for r in range(3) if not tie[r]])
+    # a NaN row is not handled at this vocabulary (the reference's NaN top-k order is unspecified)
+    y = x.copy()
+    y[0, 5] = np.nan
+    g, _ = run(sampler, O.QWEN, y[:1], None, [0.5], bf16=True, temperature=0.8, top_k=50, top_p=0.9, penalty=1.0)
+    assert g["status"][0] == _lib.TC_EUNSUPPORTED
