@@ -41,11 +41,13 @@ __device__ __forceinline__ float exp_approx(float d) { return tc_expf_fast(d); }
 constexpr float kSeqErr = 0x1p-21f;
 
 struct SeqFastLds {
-  static constexpr int kCap = 512;
+  static constexpr int kCap = 1024;
   float x[kCap];      // listed element: its input (exact term not yet known) or its exact term
   float P[kCap];      // the prediction of the running sum before it
   uint32_t q[kCap];   // integer contributions of the safe elements before it (mod 2^32)
   uint32_t info[kCap];  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: position
+  float ua[kCap];     // the replay's walk: exact terms of the elements that stay listed
+  uint32_t uq[kCap];  // and the integer contributions before each of them
   float wsum[kMaxWaves];
   uint32_t wcnt[kMaxWaves];
   uint32_t wq[kMaxWaves];
@@ -215,12 +217,14 @@ struct SeqSum {
     return true;
   }
 
-  // Wave 0 only.
+  // Wave 0 only.  First, per chunk of 64 listed elements in parallel: the
+  // exact terms, the undecided ones classified again (safe ones fold into the
+  // integer sums, a wave scan), the rest compacted into ua/uq.  Then one walk
+  // over ua/uq in element order, reading LDS by broadcast.
   template <class F>
   __device__ __forceinline__ void replay(F f, SeqFastLds& L) const {
     const int lane = lane_id();
-    float s = -0.0f;
-    uint32_t qp = 0, bad = 0, fold = 0;
+    uint32_t fold = 0, nu = 0;
     for (uint32_t base = 0; base < c_tot; base += kWave) {
       const uint32_t k = base + (uint32_t)lane;
       const bool in = k < c_tot;
@@ -233,21 +237,54 @@ struct SeqSum {
       const bool safe = in && (info & 2u) && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
       const uint32_t rs = safe ? rk : 0u;
       const uint32_t R = dpp_scan_u32(rs) + fold;  // folded contributions up to and including k
-      const uint32_t qk = (in ? L.q[k] : 0u) + (R - rs);
       fold = rl_u32(R, kWave - 1);
-      uint64_t walk = __ballot(in && !safe);
-      while (walk) {
-        const int j = __builtin_ctzll(walk);
-        walk &= walk - 1;
-        const uint32_t qj = rl_u32(qk, j);
-        const float aj = rl_f32(a, j);
-        const uint32_t d = qj - qp;
-        const float s2 = u2f(f2u(s) + d);
-        bad |= (d != 0u && (!(s > 0.0f) || (f2u(s2) >> 23) != (f2u(s) >> 23))) ? 1u : 0u;
-        s = (d != 0u ? s2 : s) + aj;
-        qp = qj;
+      const bool keep = in && !safe;
+      const uint64_t km = __ballot(keep);
+      if (keep) {
+        const uint32_t j = nu + (uint32_t)__popcll(km & ((1ull << lane) - 1ull));
+        L.ua[j] = a;
+        L.uq[j] = L.q[k] + (R - rs);
+      }
+      nu += (uint32_t)__popcll(km);
+    }
+    lds_wait();
+    // the walk: s = s + d ulps (same binade), then s = s + a, for every kept
+    // element.  Each chunk of 64 sits in lane registers (d as differences of
+    // uq, 0 and +0 past the end: adding them changes nothing) and the chain
+    // reads them with readlane, two dependent adds per element.
+    // The checks run without branches: xb = max over the elements of
+    // sb ^ (sb + d), at least 2^23 when an ulp step leaves the binade (0 for
+    // d = 0).  The terms are +0 or positive, so a step from a zero sum is one
+    // whose d is the first nonzero d with no positive term before it: two
+    // ballots per chunk find it.
+    float s = -0.0f;
+    uint32_t qp = 0, bad = 0, xb = 0;
+    bool pos = false;  // a positive term or a nonzero d seen in an earlier chunk
+    for (uint32_t base = 0; base < nu; base += kWave) {
+      const uint32_t k = base + (uint32_t)lane;
+      const bool in = k < nu;
+      const uint32_t qk = in ? L.uq[k] : 0u;
+      const uint32_t qprev = in ? (k == 0 ? 0u : L.uq[k - 1]) : 0u;
+      const uint32_t dv = in ? qk - qprev : 0u;
+      const float av = in ? L.ua[k] : 0.0f;
+      const uint64_t md = __ballot(dv != 0u), ma = __ballot(av > 0.0f);
+      if (!pos && md != 0ull && (ma & ((md & (0ull - md)) - 1ull)) == 0ull) bad = 1u;
+      pos = pos || md != 0ull || ma != 0ull;
+#pragma unroll
+      for (int g = 0; g < kWave / 16; ++g) {
+        if (base + (uint32_t)(g * 16) >= nu) break;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t di = rl_u32(dv, g * 16 + i);
+          const float ai = rl_f32(av, g * 16 + i);
+          const uint32_t sb = f2u(s), sb2 = sb + di;
+          xb = max(xb, sb ^ sb2);
+          s = u2f(sb2) + ai;
+        }
       }
     }
+    if (xb >= (1u << 23)) bad = 1u;
+    qp = nu ? L.uq[nu - 1] : 0u;
     const uint32_t d = q_tot + fold - qp;
     if (d != 0u) {
       const float s2 = u2f(f2u(s) + d);
