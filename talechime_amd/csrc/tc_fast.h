@@ -97,9 +97,9 @@ __device__ __forceinline__ float seq_tau(int pos) {
 //                 the integer sums), then one walk over the rest; writes
 //                 L.S / L.bad
 // Thread t holds ITEMS terms at element positions pos0 + i (threads in
-// order, positions increasing).  ap[i]: the term, exact where bit i of
-// exact_mask is set (invalid positions: an exact 0), otherwise within kSeqErr
-// of the exact term f(x[i]); bits of `force` are undecided whatever ap holds.
+// order, positions increasing).  ap[i]: the term, an exact +0 where bit i of
+// exact_mask is set (positions outside the row), otherwise within kSeqErr of
+// the exact term f(x[i]); bits of `force` are undecided whatever ap holds.
 template <int ITEMS>
 struct SeqSum {
   float D, ex;
@@ -144,33 +144,59 @@ struct SeqSum {
     const bool uni = P0 > 0.0f && pb0 >= 0x0b800000u && pb0 < 0x4b000000u && P0 * m_lo >= __uint_as_float(eb0) &&
                      (P0 + D) * (m_hi + 0x1p-20f) < __uint_as_float(eb0 + 0x00800000u);
     if (__ballot(!uni) == 0ull) {
+      // r = round-half-even(t / 2^(e-23)) is read from the bits of the f32 sum
+      // 2^23 + t * 2^(23-e) (2^23 plus that integer; 2^24 reads as 2^23).  The
+      // exact term lies strictly between ap * (1 -+ 2^-20) after the product's
+      // own rounding (kSeqErr is 2^-21), so both ends giving the same bits
+      // settle the rounding; a tie always lies between ends that differ.  The
+      // range stays below 2^e, so t * 2^(23-e) < 2^23.
       const float scale = __uint_as_float(0x8a800000u - eb0);  // 2^(23-e)
+      const float c_lo = scale * (1.0f - 2.0f * kSeqErr), c_hi = scale * (1.0f + 2.0f * kSeqErr);
+      uint32_t dif = 0;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
-        const float q = ap[i] * scale;
-        const float fl = __builtin_floorf(q), fr = q - fl;
-        const bool ex_i = (exact_mask >> i) & 1u;
-        const bool am = !ex_i && __builtin_fabsf(fr - 0.5f) <= q * (2.0f * kSeqErr) + 0x1p-24f;
-        r[i] = (uint32_t)fl + (fr > 0.5f ? 1u : 0u);
-        amb |= (am ? 1u : 0u) << i;
-        unsafe |= (!am && fr == 0.5f ? 1u : 0u) << i;
+        const uint32_t th = f2u(0x1p23f + ap[i] * c_hi), tl = f2u(0x1p23f + ap[i] * c_lo);
+        dif += th ^ tl;
+        r[i] = th - 0x4b000000u;
       }
-    } else {
+      if (__ballot(dif != 0u) != 0ull) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i)
+          amb |= (f2u(0x1p23f + ap[i] * c_lo) - 0x4b000000u != r[i] ? 1u : 0u) << i;
+      }
+    } else if (P0 > 0.0f && pb0 >= 0x0b800000u && (P0 + D) * m_hi < 0x1p23f) {
+      // element by element: the binade of the prediction P before it must
+      // hold P and the sum after it for every value tau allows (+0 terms
+      // never move the sum); the rounding as in the short form
       float P = P0;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
         const float Pn = P + ap[i];
-        const uint32_t c = seq_classify(P, Pn, ap[i], (exact_mask >> i) & 1u, m_lo, m_hi, &r[i]);
-        amb |= (c == 1u ? 1u : 0u) << i;
-        unsafe |= (c == 2u ? 1u : 0u) << i;
+        const uint32_t eb = f2u(P) & 0x7f800000u;
+        const bool inb = (P * m_lo >= u2f(eb) && Pn * m_hi < u2f(eb + 0x00800000u)) || ap[i] == 0.0f;
+        const float scale = u2f(0x8a800000u - eb);
+        const uint32_t th = f2u(0x1p23f + ap[i] * (scale * (1.0f + 2.0f * kSeqErr)));
+        const uint32_t tl = f2u(0x1p23f + ap[i] * (scale * (1.0f - 2.0f * kSeqErr)));
+        r[i] = th - 0x4b000000u;
+        unsafe |= (inb ? 0u : 1u) << i;
+        amb |= (th != tl ? 1u : 0u) << i;
         P = Pn;
       }
+    } else {
+      // a zero or out-of-range prediction: every element is listed
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) r[i] = 0u;
+      unsafe = (1u << ITEMS) - 1u;
     }
     amb &= ~unsafe;
     listed = unsafe | amb;
     rsum = 0;
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) rsum += ((listed >> i) & 1u) ? 0u : r[i];
+    for (int i = 0; i < ITEMS; ++i) rsum += r[i];
+    if (listed) {
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i) rsum -= ((listed >> i) & 1u) ? r[i] : 0u;
+    }
     cnt = (uint32_t)__builtin_popcount(listed);
     ci = dpp_scan_u32(cnt);
     qi = dpp_scan_u32(rsum);
