@@ -649,10 +649,11 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       F.wfin[wave_id()] = fsum;
     }
     lds_barrier();
-    float mx = F.wmax[0], fin = 0.0f;
-    for (int w = 0; w < num_waves(); ++w) {
-      mx = mx > F.wmax[w] ? mx : F.wmax[w];
-      fin += F.wfin[w];
+    float mx, fin;
+    {
+      const bool in = lane_id() < num_waves();
+      mx = dpp_wave_max(in ? F.wmax[lane_id()] : -__builtin_inff());
+      fin = dpp_wave_sum(in ? F.wfin[lane_id()] : 0.0f);
     }
     if (__builtin_isfinite(fin) && __builtin_isfinite(mx)) {
       // ids in the history, bit i = element e0 + i
@@ -682,6 +683,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       sq.predict(ap, F.seq);
       lds_barrier();
       sq.classify(ap, exm, force, e0, F.seq);
+      const float Sp = sq.total(F.seq);  // cross-lane: all lanes, before any divergence
       // Candidates, staged while the exact sum is finished.  The histogram of
       // per-thread maxima of d over ids not in the history puts the K-th largest
       // such d above -(b0 + 1) / 4; x' = d - L is monotone in d for those ids, so
@@ -697,7 +699,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
         const float thr_d = -(float)(b0 + 1u) * 0.25f - 0x1p-9f;
         float L_lo = 0.0f, L_hi = 0.0f;
         if (seen) {
-          const float Sp = sq.total(F.seq), tt = seq_tau(V);
+          const float tt = seq_tau(V);
           L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f;
           L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
         }
@@ -713,12 +715,9 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
       lds_barrier();
       const bool listed_ok = sq.write_list(ap, d, e0, F.seq);
-      uint32_t off = ci - c, n = 0;
-      for (int w = 0; w < num_waves(); ++w) {
-        const uint32_t cw = F.wcand[w];
-        off += w < wave_id() ? cw : 0u;
-        n += cw;
-      }
+      uint32_t off, n;
+      wave_table_u32(F.wcand, &off, &n);
+      off += ci - c;
       if (reach && n <= (uint32_t)FinLds::kCap) {
 #pragma unroll
         for (int i = 0; i < ITEMS; ++i)

@@ -21,6 +21,25 @@ __device__ __forceinline__ void lds_barrier() {
 }
 __device__ __forceinline__ void lds_wait() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// A per-wave table of num_waves() entries in LDS: the sum over the waves
+// before this one and over all of them.  Lane w reads entry w; a DPP scan
+// and two readlanes (one LDS round trip, no per-wave loop).  Cross-lane:
+// call with every lane of the wave active.
+__device__ __forceinline__ void wave_table_u32(const uint32_t* tab, uint32_t* before, uint32_t* all) {
+  const uint32_t v = lane_id() < num_waves() ? tab[lane_id()] : 0u;
+  const uint32_t inc = dpp_scan_u32(v);
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());
+  *before = wv > 0 ? rl_u32(inc, wv - 1) : 0u;
+  *all = rl_u32(inc, kWave - 1);
+}
+__device__ __forceinline__ void wave_table_f32(const float* tab, float* before, float* all) {
+  const float v = lane_id() < num_waves() ? tab[lane_id()] : 0.0f;
+  const float inc = dpp_scan_f32(v);
+  const int wv = __builtin_amdgcn_readfirstlane(wave_id());
+  *before = wv > 0 ? rl_f32(inc, wv - 1) : 0.0f;
+  *all = rl_f32(inc, kWave - 1);
+}
+
 // exp(d) for d in [-87, 0]: tc_expf_fast, within 1 ulp of the correctly
 // rounded value (checked for every input by the table generator); glibc's
 // expf is within 1 ulp of it too, so kSeqErr = 2^-21 bounds the relative
@@ -43,12 +62,13 @@ constexpr float kSeqErr = 0x1p-21f;
 struct SeqFastLds {
   static constexpr int kCap = 1024;
   float x[kCap];      // listed element: its input (exact term not yet known) or its exact term
-  float P[kCap];      // the prediction of the running sum before it
+  float P[kCap];      // the refined prediction of the running sum before it
   uint32_t q[kCap];   // integer contributions of the safe elements before it (mod 2^32)
   uint32_t info[kCap];  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: position
   float ua[kCap];     // the replay's walk: exact terms of the elements that stay listed
   uint32_t uq[kCap];  // and the integer contributions before each of them
   float wsum[kMaxWaves];
+  float wp2[kMaxWaves];  // wave totals of the refined prediction
   uint32_t wcnt[kMaxWaves];
   uint32_t wq[kMaxWaves];
   float S;
@@ -58,11 +78,12 @@ struct SeqFastLds {
 // Classification of one element, without branches: 0 = safe (*r set: the
 // element adds *r ulps of its binade), 1 = the approximate term cannot decide
 // the rounding, 2 = listed (first positive term, binade crossing, tie, or a
-// running sum outside [2^-104, 2^23)).
+// running sum outside [2^-90, 2^23): below 2^-90 the terms under the
+// approximation's range, each within 2^-125 of theirs, could matter).
 __device__ __forceinline__ uint32_t seq_classify(float P, float Pn, float a, bool exact, float m_lo, float m_hi,
                                                  uint32_t* r) {
   const uint32_t pb = __float_as_uint(P);
-  const bool ok_p = P > 0.0f && pb >= 0x0b800000u && pb < 0x4b000000u;
+  const bool ok_p = P > 0.0f && pb >= 0x12800000u && pb < 0x4b000000u;
   const uint32_t eb = ok_p ? (pb & 0x7f800000u) : 0x3f800000u;
   const float lo = __uint_as_float(eb), hi = __uint_as_float(eb + 0x00800000u);
   const bool inb = ok_p && P * m_lo >= lo && Pn * m_hi < hi;
@@ -88,14 +109,23 @@ __device__ __forceinline__ float seq_tau(int pos) {
 //   -- barrier --
 //   classify()    the prediction P0 of each thread; grid rounding of every
 //                 element; the list of undecided and listed elements and its
-//                 (count, integer sum) wave scans; writes L.wcnt / L.wq
+//                 (count, integer sum, refined prediction) wave scans;
+//                 writes L.wcnt / L.wq / L.wp2
 //   -- barrier --
 //   write_list()  list offsets; writes the list (false: more than kCap)
 //   -- barrier --
 //   replay()      wave 0: the exact terms of the listed elements in parallel,
-//                 the undecided ones classified again (safe ones fold into
-//                 the integer sums), then one walk over the rest; writes
-//                 L.S / L.bad
+//                 each classified again against the refined prediction
+//                 (safe ones fold into the integer sums), then one walk over
+//                 the rest; writes L.S / L.bad
+// The refined prediction P2 before a listed element is the sum of what the
+// elements before it add: r ulps of the binade for a safe element of a
+// short-form thread (exactly what the sequential sum adds) and the
+// approximate term for every other element.  Its distance from the
+// sequential sum comes from the u elements of the second kind before it
+// (each rounds by at most half an ulp of the sum, 2^-24 relative, and its
+// term is within kSeqErr) and at most 48 f32 adds, so seq_tau(u) bounds it as
+// seq_tau(pos) bounds the first prediction.
 // Thread t holds ITEMS terms at element positions pos0 + i (threads in
 // order, positions increasing).  ap[i]: the term, an exact +0 where bit i of
 // exact_mask is set (positions outside the row), otherwise within kSeqErr of
@@ -107,6 +137,8 @@ struct SeqSum {
   uint32_t r[ITEMS];
   uint32_t listed, amb, exact;
   uint32_t cnt, rsum, ci, qi;
+  float T, ex2;  // refined prediction: this thread's share and its wave-exclusive prefix
+  float ulp0;    // short form: the ulp of the thread's binade (0: elements checked one by one)
   uint32_t c_tot, q_tot;
 
   __device__ __forceinline__ void predict(const float (&ap)[ITEMS], SeqFastLds& L) {
@@ -118,18 +150,19 @@ struct SeqSum {
     if (lane_id() == kWave - 1) L.wsum[wave_id()] = inc;
   }
 
-  // The prediction of the whole sum (valid after the first barrier).
+  // The prediction of the whole sum (valid after the first barrier; every
+  // lane of the wave active).
   __device__ __forceinline__ float total(const SeqFastLds& L) const {
-    float t = 0.0f;
-    for (int w = 0; w < num_waves(); ++w) t += L.wsum[w];
+    float b, t;
+    wave_table_f32(L.wsum, &b, &t);
     return t;
   }
 
   __device__ __forceinline__ void classify(const float (&ap)[ITEMS], uint32_t exact_mask, uint32_t force, int pos0,
                                            SeqFastLds& L) {
     const int wv = wave_id();
-    float off = 0.0f;
-    for (int w = 0; w < wv; ++w) off += L.wsum[w];
+    float off, all;
+    wave_table_f32(L.wsum, &off, &all);
     P0 = off + ex;
     exact = exact_mask;
     const float tau = seq_tau(pos0 + ITEMS);
@@ -141,9 +174,12 @@ struct SeqSum {
     // threads can (no divergence inside a wave)
     const uint32_t pb0 = __float_as_uint(P0);
     const uint32_t eb0 = pb0 & 0x7f800000u;
-    const bool uni = P0 > 0.0f && pb0 >= 0x0b800000u && pb0 < 0x4b000000u && P0 * m_lo >= __uint_as_float(eb0) &&
+    const bool uni = P0 > 0.0f && pb0 >= 0x12800000u && pb0 < 0x4b000000u && P0 * m_lo >= __uint_as_float(eb0) &&
                      (P0 + D) * (m_hi + 0x1p-20f) < __uint_as_float(eb0 + 0x00800000u);
+    ulp0 = 0.0f;
+    T = D;
     if (__ballot(!uni) == 0ull) {
+      ulp0 = __uint_as_float(eb0 - 0x0b800000u);
       // r = round-half-even(t / 2^(e-23)) is read from the bits of the f32 sum
       // 2^23 + t * 2^(23-e) (2^23 plus that integer; 2^24 reads as 2^23).  The
       // exact term lies strictly between ap * (1 -+ 2^-20) after the product's
@@ -164,7 +200,7 @@ struct SeqSum {
         for (int i = 0; i < ITEMS; ++i)
           amb |= (f2u(0x1p23f + ap[i] * c_lo) - 0x4b000000u != r[i] ? 1u : 0u) << i;
       }
-    } else if (P0 > 0.0f && pb0 >= 0x0b800000u && (P0 + D) * m_hi < 0x1p23f) {
+    } else if (P0 > 0.0f && pb0 >= 0x12800000u && (P0 + D) * m_hi < 0x1p23f) {
       // element by element: the binade of the prediction P before it must
       // hold P and the sum after it for every value tau allows (+0 terms
       // never move the sum); the rounding as in the short form
@@ -197,43 +233,62 @@ struct SeqSum {
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) rsum -= ((listed >> i) & 1u) ? r[i] : 0u;
     }
-    cnt = (uint32_t)__builtin_popcount(listed);
+    // The refined prediction: in the short form safe elements add exactly r
+    // ulps of the binade to the sequential sum and listed ones their
+    // approximate term; elements checked one by one enter with their
+    // approximate terms, and each counts in the bound like a listed one
+    // (bits 16+ of cnt; the list count is bits 0-15).
+    uint32_t slack = 0;
+    if (ulp0 != 0.0f) {
+      T = (float)rsum * ulp0;
+      if (listed) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) T += ((listed >> i) & 1u) ? ap[i] : 0.0f;
+      }
+    } else if (listed != (1u << ITEMS) - 1u) {
+      slack = ITEMS;
+    }
+    const float t2 = dpp_scan_f32(T);
+    ex2 = dpp_prev_f32(t2);
+    cnt = (uint32_t)__builtin_popcount(listed) | (slack << 16);
     ci = dpp_scan_u32(cnt);
     qi = dpp_scan_u32(rsum);
     if (lane_id() == kWave - 1) {
       L.wcnt[wv] = ci;
       L.wq[wv] = qi;
+      L.wp2[wv] = t2;
     }
   }
 
   __device__ __forceinline__ bool write_list(const float (&ap)[ITEMS], const float (&x)[ITEMS], int pos0,
                                              SeqFastLds& L) {
-    const int wv = wave_id();
-    uint32_t c_off = ci - cnt, q_off = qi - rsum;
-    c_tot = 0;
-    q_tot = 0;
-    for (int w = 0; w < num_waves(); ++w) {
-      const uint32_t wc = L.wcnt[w], wq = L.wq[w];
-      if (w < wv) {
-        c_off += wc;
-        q_off += wq;
-      }
-      c_tot += wc;
-      q_tot += wq;
-    }
+    uint32_t c_off, q_off;
+    float p2, p2_all;
+    wave_table_u32(L.wcnt, &c_off, &c_tot);
+    wave_table_u32(L.wq, &q_off, &q_tot);
+    wave_table_f32(L.wp2, &p2, &p2_all);
+    c_off += ci - cnt;
+    q_off += qi - rsum;
+    p2 += ex2;
+    const uint32_t g = c_off >> 16;  // uncertainty count of the threads before
+    c_off &= 0xffffu;
+    c_tot &= 0xffffu;
     if (c_tot > (uint32_t)SeqFastLds::kCap) return false;
     if (listed) {
       uint32_t k = c_off, q = q_off;
-      float P = P0;
+      float P = P0, al = 0.0f;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
         if ((listed >> i) & 1u) {
           const bool exa = (exact >> i) & 1u;
           L.x[k] = exa ? ap[i] : x[i];
-          L.P[k] = P;
+          L.P[k] = p2 + (ulp0 != 0.0f ? (float)(q - q_off) * ulp0 + al : P - P0);
           L.q[k] = q;
-          L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | ((uint32_t)(pos0 + i) << 8);
+          // bits 8+: the uncertainty count of the refined prediction
+          const uint32_t u = k + g + (ulp0 != 0.0f ? 0u : (uint32_t)i);
+          L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | (u << 8);
           ++k;
+          al += ap[i];
         } else {
           q += r[i];
         }
@@ -260,7 +315,7 @@ struct SeqSum {
       const float a = (info & 1u) ? xin : f(xin);
       uint32_t rk = 0;
       const float tk = seq_tau((int)(info >> 8));
-      const bool safe = in && (info & 2u) && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
+      const bool safe = in && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
       const uint32_t rs = safe ? rk : 0u;
       const uint32_t R = dpp_scan_u32(rs) + fold;  // folded contributions up to and including k
       fold = rl_u32(R, kWave - 1);
