@@ -580,6 +580,8 @@ struct IdxFastLds {
   float wmax[kMaxWaves];
   float wfin[kMaxWaves];
   uint32_t wcand[kMaxWaves];
+  double lnref, invref;  // log and reciprocal of fref, the refined prediction of the sum
+  float fref;
   SeqFastLds seq;
   FinLds fin;
 };
@@ -697,17 +699,25 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       if (reach) {
         const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
         const float thr_d = -(float)(b0 + 1u) * 0.25f - 0x1p-9f;
-        float L_lo = 0.0f, L_hi = 0.0f;
-        if (seen) {
+        // an id in the history reaches the bound for some L in [L_lo, L_hi]
+        // when (d - L_lo) * pen >= thr_d - L_hi, i.e. (pen > 0) d >= thr_s,
+        // taken a margin far above its roundings lower
+        float thr_s = -__builtin_inff();
+        if (a.do_pen && a.pen_f > 0.0f) {
           const float tt = seq_tau(V);
-          L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f;
-          L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
+          const float L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f, L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
+          thr_s = L_lo + (thr_d - L_hi) / a.pen_f - 0x1p-9f;
         }
+        // one compare per element against the lower threshold; the few hits
+        // are then held to their own
+        const float thr_lo = thr_s < thr_d ? thr_s : thr_d;
 #pragma unroll
-        for (int i = 0; i < ITEMS; ++i) {
-          const bool v = (vm >> i) & 1u, sn = (seen >> i) & 1ull;
-          const bool ok = sn ? ((d[i] - L_lo) * a.pen_f >= thr_d - L_hi) : d[i] >= thr_d;
-          sel |= (v && ok ? 1u : 0u) << i;
+        for (int i = 0; i < ITEMS; ++i) sel |= (d[i] >= thr_lo ? 1u : 0u) << i;
+        sel &= vm;
+        if (sel) {
+#pragma unroll
+          for (int i = 0; i < ITEMS; ++i)
+            sel &= ~((d[i] >= (((seen >> i) & 1ull) ? thr_s : thr_d) ? 0u : 1u) << i);
         }
       }
       const uint32_t c = (uint32_t)__builtin_popcount(sel);
@@ -715,6 +725,13 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
       lds_barrier();
       const bool listed_ok = sq.write_list(ap, d, e0, F.seq);
+      // the exception keys of glibc logf around the expected sum, in flight
+      // while the sum is finished
+      LogfKeys lk;
+      if (wave_id() == 0) {
+        const float tt = seq_tau((int)sq.u_tot) + 0x1p-22f;
+        logf_keys_index(lk, sq.p2_tot * (1.0f - tt), sq.p2_tot * (1.0f + tt));
+      }
       uint32_t off, n;
       wave_table_u32(F.wcand, &off, &n);
       off += ci - c;
@@ -725,7 +742,20 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
             F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) |
                                 (uint32_t)(e0 + i);
         lds_barrier();
-        if (listed_ok && wave_id() == 0) sq.replay([](float v) { return expf_glibc(v); }, F.seq);
+        if (listed_ok) sq.replay_terms([](float v) { return expf_glibc(v); }, F.seq);
+        lds_barrier();
+        // wave 1, idle during the walk: log and reciprocal of the refined
+        // prediction of the sum, from which wave 0 gets the log of the sum
+        if (wave_id() == 1 && lane_id() == 0) {
+          const float ref = (sq.p2_tot >= 1.0f && sq.p2_tot < 16777216.0f) ? sq.p2_tot : 1.0f;
+          F.fref = ref;
+          F.lnref = tc_log_d((double)ref);
+          F.invref = 1.0 / (double)ref;
+        }
+        if (wave_id() == 0) {
+          logf_keys_load(lk);
+          if (listed_ok) sq.replay_walk(F.seq);
+        }
         lds_barrier();
         float S = F.seq.S;
         if (!listed_ok || F.seq.bad) {
@@ -736,7 +766,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
           S = block_seqsum_slow<ITEMS>(ex, e0, V, F.seq.x, SeqFastLds::kCap, &F.seq.S);
         }
         if (wave_id() == 0) {
-          const float L = logf_glibc(S);
+          const float L = logf_glibc_near(S, F.fref, F.lnref, F.invref, lk);
           put_norm(a, row, L);
           idx_fast_finish(a, row, n, L, F.fin);
         }

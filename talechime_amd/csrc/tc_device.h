@@ -85,6 +85,36 @@ __device__ __forceinline__ bool logf_is_exception(uint32_t b) {
   return false;
 }
 
+// The exception keys of the buckets holding [s_lo, s_hi] in lane registers of
+// one wave (lane j: key lo + j), fetched ahead of a logf_glibc_keys call
+// whose argument is expected in that range: the index entries first
+// (logf_keys_index), the keys once those have arrived (logf_keys_load).
+// Every lane of the wave active throughout.
+struct LogfKeys {
+  uint32_t b0, nb, lo, n;  // wave-uniform
+  uint32_t idx, key;       // per lane
+  bool ok;
+};
+__device__ __forceinline__ void logf_keys_index(LogfKeys& K, float s_lo, float s_hi) {
+  s_lo = s_lo > 1.0f ? s_lo : 1.0f;
+  const uint32_t b0 = (f2u(s_lo) - 0x3f800000u) >> TC_LOGF_BUCKET_SHIFT;
+  const uint32_t b1 = (f2u(s_hi) - 0x3f800000u) >> TC_LOGF_BUCKET_SHIFT;
+  K.ok = s_hi >= s_lo && s_hi < 16777216.0f && b1 < TC_LOGF_NBUCKETS && b1 - b0 < 63u;
+  K.b0 = b0;
+  K.nb = b1 - b0 + 1u;
+  const uint32_t j = threadIdx.x & 63u;
+  K.idx = (K.ok && j <= K.nb) ? tc_logf_exc_index[b0 + j] : 0u;
+}
+__device__ __forceinline__ void logf_keys_load(LogfKeys& K) {
+  if (K.ok) {
+    K.lo = (uint32_t)__builtin_amdgcn_readlane((int)K.idx, 0);
+    K.n = (uint32_t)__builtin_amdgcn_readlane((int)K.idx, (int)K.nb) - K.lo;
+    K.ok = K.n <= 64u;
+  }
+  const uint32_t j = threadIdx.x & 63u;
+  K.key = (K.ok && j < K.n) ? tc_logf_exc_keys[K.lo + j] : 0xffffffffu;  // a NaN: never a key
+}
+
 // Rust's f32::ln (glibc logf) for x in [1, 2^24); other inputs get the
 // correctly rounded value.
 __device__ __forceinline__ float logf_glibc(float x) {
@@ -93,6 +123,49 @@ __device__ __forceinline__ float logf_glibc(float x) {
   double y = tc_log_d((double)x);
   float r = (float)y;
   if (tc_mid_dist(y, r) < TC_LOGF_BAND && logf_is_exception(f2u(x))) r = u2f(tc_toward(y, r));
+  return r;
+}
+// The same with x wave-uniform and the keys of its bucket, when K covers it,
+// read from K (every lane of the wave active).
+__device__ __forceinline__ float logf_glibc_keys(float x, const LogfKeys& K) {
+  if (!(x >= 1.0f && x < 16777216.0f)) return tc_logf_cr(x);
+  if (x == 1.0f) return 0.0f;
+  double y = tc_log_d((double)x);
+  float r = (float)y;
+  if (tc_mid_dist(y, r) < TC_LOGF_BAND) {
+    const uint32_t b = f2u(x), bk = (b - 0x3f800000u) >> TC_LOGF_BUCKET_SHIFT;
+    const bool exc = (K.ok && bk >= K.b0 && bk - K.b0 < K.nb) ? __ballot(K.key == b) != 0ull : logf_is_exception(b);
+    if (exc) r = u2f(tc_toward(y, r));
+  }
+  return r;
+}
+
+// logf_glibc_keys(x, K) from ln_ref = tc_log_d(ref) and inv_ref = 1 / ref
+// for a float ref near x: log x = ln_ref + log1p((x - ref) / ref), the series
+// to the fifth power (|d| < 2^-10: the rest is below 2^-60).  This y and
+// tc_log_d(x) are both within a few 2^-53 relative of log x, so they differ
+// by less than err = 2^-48 (|ln_ref| + |log1p|): farther than err from a
+// rounding midpoint both round alike, and every input whose tc_log_d lies
+// inside the exception band lies within band + err here.  Near a midpoint,
+// or with ref far from x, the reference computation.  x wave-uniform, every
+// lane active.
+__device__ __forceinline__ float logf_glibc_near(float x, float ref, double ln_ref, double inv_ref,
+                                                 const LogfKeys& K) {
+  if (!(x > 1.0f && x < 16777216.0f)) return logf_glibc_keys(x, K);
+  const double dd = ((double)x - (double)ref) * inv_ref;
+  if (!(__builtin_fabs(dd) < 0x1p-10)) return logf_glibc_keys(x, K);
+  const double lp = dd * (1.0 - dd * (0.5 - dd * (1.0 / 3.0 - dd * (0.25 - dd * 0.2))));
+  const double y = ln_ref + lp;
+  const float r = (float)y;
+  const uint32_t nbb = tc_toward(y, r);
+  const double gap = __builtin_fabs((double)u2f(nbb) - (double)r), mid = 0.5 * ((double)u2f(nbb) + (double)r);
+  const double dist = __builtin_fabs(y - mid), err = 0x1p-48 * (__builtin_fabs(ln_ref) + __builtin_fabs(lp));
+  if (!(dist > err)) return logf_glibc_keys(x, K);
+  if (dist < TC_LOGF_BAND * gap + err) {
+    const uint32_t b = f2u(x), bk = (b - 0x3f800000u) >> TC_LOGF_BUCKET_SHIFT;
+    const bool exc = (K.ok && bk >= K.b0 && bk - K.b0 < K.nb) ? __ballot(K.key == b) != 0ull : logf_is_exception(b);
+    if (exc) return u2f(nbb);
+  }
   return r;
 }
 

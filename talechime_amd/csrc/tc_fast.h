@@ -65,8 +65,11 @@ struct SeqFastLds {
   float P[kCap];      // the refined prediction of the running sum before it
   uint32_t q[kCap];   // integer contributions of the safe elements before it (mod 2^32)
   uint32_t info[kCap];  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: position
-  float ua[kCap];     // the replay's walk: exact terms of the elements that stay listed
-  uint32_t uq[kCap];  // and the integer contributions before each of them
+  float ua[kCap];     // the replay's walk: exact terms of the elements that stay listed,
+  uint32_t uq[kCap];  // compacted inside each chunk of 64, and the integer
+                      // contributions before each (less the earlier chunks' folds)
+  uint32_t cf[kCap / kWave];  // per chunk: the integer contributions folded in
+  uint32_t ck[kCap / kWave];  // and the number of elements kept
   float wsum[kMaxWaves];
   float wp2[kMaxWaves];  // wave totals of the refined prediction
   uint32_t wcnt[kMaxWaves];
@@ -114,10 +117,11 @@ __device__ __forceinline__ float seq_tau(int pos) {
 //   -- barrier --
 //   write_list()  list offsets; writes the list (false: more than kCap)
 //   -- barrier --
-//   replay()      wave 0: the exact terms of the listed elements in parallel,
-//                 each classified again against the refined prediction
-//                 (safe ones fold into the integer sums), then one walk over
-//                 the rest; writes L.S / L.bad
+//   replay_terms() every wave, a chunk of 64 listed elements each: their
+//                 exact terms, each classified again against the refined
+//                 prediction (safe ones fold into the integer sums)
+//   -- barrier --
+//   replay_walk() wave 0: one walk over the rest; writes L.S / L.bad
 // The refined prediction P2 before a listed element is the sum of what the
 // elements before it add: r ulps of the binade for a safe element of a
 // short-form thread (exactly what the sequential sum adds) and the
@@ -138,6 +142,8 @@ struct SeqSum {
   uint32_t listed, amb, exact;
   uint32_t cnt, rsum, ci, qi;
   float T, ex2;  // refined prediction: this thread's share and its wave-exclusive prefix
+  float p2_tot;    // refined prediction of the whole sum (after write_list)
+  uint32_t u_tot;  // and its uncertainty count: seq_tau(u_tot) bounds it
   float ulp0;    // short form: the ulp of the thread's binade (0: elements checked one by one)
   uint32_t c_tot, q_tot;
 
@@ -272,7 +278,9 @@ struct SeqSum {
     p2 += ex2;
     const uint32_t g = c_off >> 16;  // uncertainty count of the threads before
     c_off &= 0xffffu;
+    u_tot = (c_tot & 0xffffu) + (c_tot >> 16);
     c_tot &= 0xffffu;
+    p2_tot = p2_all;
     if (c_tot > (uint32_t)SeqFastLds::kCap) return false;
     if (listed) {
       uint32_t k = c_off, q = q_off;
@@ -298,16 +306,16 @@ struct SeqSum {
     return true;
   }
 
-  // Wave 0 only.  First, per chunk of 64 listed elements in parallel: the
-  // exact terms, the undecided ones classified again (safe ones fold into the
-  // integer sums, a wave scan), the rest compacted into ua/uq.  Then one walk
-  // over ua/uq in element order, reading LDS by broadcast.
+  // Every wave, chunks wave, wave + num_waves(), ... of 64 listed elements,
+  // all lanes active: the exact terms, each element classified again against
+  // the refined prediction (safe ones fold into the integer sums), the rest
+  // compacted inside the chunk into ua/uq.
   template <class F>
-  __device__ __forceinline__ void replay(F f, SeqFastLds& L) const {
+  __device__ __forceinline__ void replay_terms(F f, SeqFastLds& L) const {
     const int lane = lane_id();
-    uint32_t fold = 0, nu = 0;
-    for (uint32_t base = 0; base < c_tot; base += kWave) {
-      const uint32_t k = base + (uint32_t)lane;
+    const uint32_t nw = (uint32_t)num_waves(), wv = (uint32_t)__builtin_amdgcn_readfirstlane(wave_id());
+    for (uint32_t c = wv; c * kWave < c_tot; c += nw) {
+      const uint32_t k = c * kWave + (uint32_t)lane;
       const bool in = k < c_tot;
       const uint32_t info = in ? L.info[k] : 1u;
       const float xin = in ? L.x[k] : 0.0f;
@@ -317,18 +325,25 @@ struct SeqSum {
       const float tk = seq_tau((int)(info >> 8));
       const bool safe = in && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
       const uint32_t rs = safe ? rk : 0u;
-      const uint32_t R = dpp_scan_u32(rs) + fold;  // folded contributions up to and including k
-      fold = rl_u32(R, kWave - 1);
+      const uint32_t R = dpp_scan_u32(rs);  // folded contributions of the chunk up to and including k
       const bool keep = in && !safe;
       const uint64_t km = __ballot(keep);
       if (keep) {
-        const uint32_t j = nu + (uint32_t)__popcll(km & ((1ull << lane) - 1ull));
+        const uint32_t j = c * kWave + (uint32_t)__popcll(km & ((1ull << lane) - 1ull));
         L.ua[j] = a;
         L.uq[j] = L.q[k] + (R - rs);
       }
-      nu += (uint32_t)__popcll(km);
+      if (lane == kWave - 1) {
+        L.cf[c] = R;
+        L.ck[c] = (uint32_t)__popcll(km);
+      }
     }
-    lds_wait();
+  }
+
+  // Wave 0 only, after replay_terms on every wave: one walk over the kept
+  // elements in element order.
+  __device__ __forceinline__ void replay_walk(SeqFastLds& L) const {
+    const int lane = lane_id();
     // the walk: s = s + d ulps (same binade), then s = s + a, for every kept
     // element.  Each chunk of 64 sits in lane registers (d as differences of
     // uq, 0 and +0 past the end: adding them changes nothing) and the chain
@@ -339,21 +354,30 @@ struct SeqSum {
     // whose d is the first nonzero d with no positive term before it: two
     // ballots per chunk find it.
     float s = -0.0f;
-    uint32_t qp = 0, bad = 0, xb = 0;
+    uint32_t qp = 0, bad = 0, xb = 0, fold = 0;
     bool pos = false;  // a positive term or a nonzero d seen in an earlier chunk
-    for (uint32_t base = 0; base < nu; base += kWave) {
-      const uint32_t k = base + (uint32_t)lane;
-      const bool in = k < nu;
-      const uint32_t qk = in ? L.uq[k] : 0u;
-      const uint32_t qprev = in ? (k == 0 ? 0u : L.uq[k - 1]) : 0u;
+    const uint32_t nch = (c_tot + kWave - 1) / kWave;
+    for (uint32_t c = 0; c < nch; ++c) {
+      const uint32_t nu = (uint32_t)__builtin_amdgcn_readfirstlane((int)L.ck[c]);
+      const uint32_t cfc = (uint32_t)__builtin_amdgcn_readfirstlane((int)L.cf[c]);
+      if (nu == 0u) {
+        fold += cfc;
+        continue;
+      }
+      const uint32_t k = c * kWave + (uint32_t)lane;
+      const bool in = (uint32_t)lane < nu;
+      const uint32_t qk = in ? L.uq[k] + fold : 0u;
+      const uint32_t qprev = in ? (lane == 0 ? qp : L.uq[k - 1] + fold) : 0u;
       const uint32_t dv = in ? qk - qprev : 0u;
       const float av = in ? L.ua[k] : 0.0f;
+      qp = rl_u32(qk, (int)nu - 1);
+      fold += cfc;
       const uint64_t md = __ballot(dv != 0u), ma = __ballot(av > 0.0f);
       if (!pos && md != 0ull && (ma & ((md & (0ull - md)) - 1ull)) == 0ull) bad = 1u;
       pos = pos || md != 0ull || ma != 0ull;
 #pragma unroll
       for (int g = 0; g < kWave / 16; ++g) {
-        if (base + (uint32_t)(g * 16) >= nu) break;
+        if ((uint32_t)(g * 16) >= nu) break;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const uint32_t di = rl_u32(dv, g * 16 + i);
@@ -365,7 +389,6 @@ struct SeqSum {
       }
     }
     if (xb >= (1u << 23)) bad = 1u;
-    qp = nu ? L.uq[nu - 1] : 0u;
     const uint32_t d = q_tot + fold - qp;
     if (d != 0u) {
       const float s2 = u2f(f2u(s) + d);
