@@ -7,7 +7,9 @@ Steps:
      csrc/_gen/expf_glibc_exc.inc and csrc/_gen/logf_glibc_exc.inc -- skipped
      when both includes are newer than the generator and tc_math.h;
   2. hipcc --offload-arch=gfx950 -shared the kernels and the C ABI into
-     talechime_amd/libtalechime_hip.so.
+     talechime_amd/libtalechime_hip.so;
+  3. the same for csrc/selftest.hip into talechime_amd/libtc_selftest.so
+     (on-device checks of the approximations, loaded by the tests only).
 
 Floating-point flags are part of the contract: no contraction (the kernels
 reproduce unfused reference arithmetic; explicit fma() stays fused), denormals
@@ -26,6 +28,7 @@ CSRC = os.path.join(PKG, "csrc")
 GEN = os.path.join(CSRC, "_gen")
 ROOT = os.path.dirname(PKG)
 LIB = os.path.join(PKG, "libtalechime_hip.so")
+SELFTEST = os.path.join(PKG, "libtc_selftest.so")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -81,9 +84,21 @@ def build_lib() -> str:
     return LIB
 
 
+def build_selftest() -> str:
+    """On-device checks of the approximations (tests load it; the sampler does not)."""
+    out_tmp = SELFTEST + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+           os.path.join(CSRC, "selftest.hip"), "-o", out_tmp]
+    subprocess.run(cmd, check=True)
+    os.replace(out_tmp, SELFTEST)
+    return SELFTEST
+
+
 def build(force_tables: bool = False) -> str:
     gen_tables(force_tables)
-    return build_lib()
+    lib = build_lib()
+    build_selftest()
+    return lib
 
 
 if __name__ == "__main__":

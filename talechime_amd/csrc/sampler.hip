@@ -742,7 +742,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
             F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) |
                                 (uint32_t)(e0 + i);
         lds_barrier();
-        if (listed_ok) sq.replay_terms([](float v) { return expf_glibc(v); }, F.seq);
+        if (listed_ok) sq.replay_terms([](float v) { return expf_glibc_wave(v); }, F.seq);
         lds_barrier();
         // wave 1, idle during the walk: log and reciprocal of the refined
         // prediction of the sum, from which wave 0 gets the log of the sum

@@ -36,6 +36,19 @@ __device__ __forceinline__ double rmaxd(double a, double b) {
   return __builtin_isnan(a) ? b : (__builtin_isnan(b) ? a : (a > b ? a : b));
 }
 
+// exp(d) for d in [-87, 0], approximate: d * log2(e), with log2(e) in two
+// floats, is p + e (p = the rounded product, e the rest to about 2^-48
+// relative, by two fmas); v_exp_f32(p) corrected to first order by
+// 1 + e ln 2.  Within 3 ulps of the correctly rounded value on every input of
+// the range (checked on the device by tc_selftest_exp_approx; the result is
+// normal, >= 2^-125.5), so within 4 ulps, 2^-21 relative, of glibc's expf.
+__device__ __forceinline__ float exp_approx(float d) {
+  constexpr float kL2eHi = 0x1.715476p+0f, kL2eLo = 0x1.4ae0cp-26f;
+  const float p = d * kL2eHi;
+  const float e = __builtin_fmaf(d, kL2eLo, __builtin_fmaf(d, kL2eHi, -p));
+  return __builtin_amdgcn_exp2f(p) * __builtin_fmaf(e, 0.693147180559945309f, 1.0f);
+}
+
 // ---------------------------------------------------------------- glibc expf
 // glibc's expf differs from the correctly rounded value only on the inputs in
 // tc_expf_exc_keys, all of which sit within TC_EXPF_BAND ulp of a rounding
@@ -62,6 +75,34 @@ __device__ __forceinline__ float expf_glibc(float x) {
   if (tc_mid_dist(y, r) < TC_EXPF_BAND) {
     if (expf_is_exception(f2u(x))) r = u2f(tc_toward(y, r));
   }
+  return r;
+}
+
+// expf_glibc of every lane's x, the lanes whose value lies in the band looked
+// up one at a time by the whole wave: the bucket's index entries (one uniform
+// load), then all of its keys at once (one load per lane) against the key,
+// instead of a binary search of dependent loads.  Every lane active.
+__device__ __forceinline__ float expf_glibc_wave(float x) {
+  const bool mid = !__builtin_isnan(x) && x >= -104.0f && x <= 88.72283935546875f;
+  const double y = tc_exp_d(mid ? (double)x : 0.0);
+  float r = (float)y;
+  const bool inb = mid && tc_mid_dist(y, r) < TC_EXPF_BAND;
+  uint64_t need = __ballot(inb);
+  const uint32_t lane = threadIdx.x & 63u;
+  while (need) {
+    const int l = __builtin_ctzll(need);
+    need &= need - 1ull;
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)f2u(x), l);
+    const uint32_t lo = tc_expf_exc_index[b >> 16], hi = tc_expf_exc_index[(b >> 16) + 1u];
+    bool exc = false;
+    for (uint32_t base = lo; base < hi; base += 64u) {
+      const uint32_t j = base + lane;
+      const uint32_t k = j < hi ? tc_expf_exc_keys[j] : ~b;
+      exc = exc || __ballot(k == b) != 0ull;
+    }
+    if (exc && lane == (uint32_t)l) r = u2f(tc_toward(y, r));
+  }
+  if (!mid) r = __builtin_isnan(x) ? x : (x < -104.0f ? 0.0f : __builtin_inff());
   return r;
 }
 

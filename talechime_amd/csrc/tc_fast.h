@@ -40,11 +40,6 @@ __device__ __forceinline__ void wave_table_f32(const float* tab, float* before, 
   *all = rl_f32(inc, kWave - 1);
 }
 
-// exp(d) for d in [-87, 0]: tc_expf_fast, within 1 ulp of the correctly
-// rounded value (checked for every input by the table generator); glibc's
-// expf is within 1 ulp of it too, so kSeqErr = 2^-21 bounds the relative
-// distance from the reference's term with a margin of 2.
-__device__ __forceinline__ float exp_approx(float d) { return tc_expf_fast(d); }
 
 // ---------------------------------------------------------------- exact sequential sum
 // The bits of s = -0.0f; for each term in element order: s = s + t (the
@@ -57,6 +52,7 @@ __device__ __forceinline__ float exp_approx(float d) { return tc_expf_fast(d); }
 // term go to a list that one wave replays exactly.  The integer
 // contributions are summed modulo 2^32: between two listed elements they stay
 // inside one binade, so every difference the replay takes is below 2^24.
+// exp_approx keeps its terms within 4 ulps (2^-21 relative) of glibc's expf.
 constexpr float kSeqErr = 0x1p-21f;
 
 struct SeqFastLds {
@@ -320,7 +316,8 @@ struct SeqSum {
       const uint32_t info = in ? L.info[k] : 1u;
       const float xin = in ? L.x[k] : 0.0f;
       const float Pk = in ? L.P[k] : 0.0f;
-      const float a = (info & 1u) ? xin : f(xin);
+      const float fx = f(xin);  // outside the select: f may need every lane
+      const float a = (info & 1u) ? xin : fx;
       uint32_t rk = 0;
       const float tk = seq_tau((int)(info >> 8));
       const bool safe = in && seq_classify(Pk, Pk + a, a, true, 1.0f - tk, 1.0f + tk, &rk) == 0u;
