@@ -431,7 +431,9 @@ struct FinLds {
 // order_margin bounds everything that separates them from the reference's
 // sequential, normalised sums, and the reference's loops run whenever a
 // decision falls inside it.
-__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
+// NS: the candidate slots per lane (1 when n <= 64; slot 1 then folds away).
+template <int NS>
+__device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
   const int lane = lane_id();
   float sc[2];
   uint32_t id[2];
@@ -440,7 +442,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const uint32_t c = (uint32_t)(q * kWave + lane);
-    has[q] = c < n;
+    has[q] = q < NS && c < n;
     const uint64_t v = has[q] ? F.cand[c] : 0ull;
     id[q] = (uint32_t)v & 0x7fffffffu;
     // log_softmax, then the penalty on the log-prob (x' <= 0: s * pen), then T
@@ -450,16 +452,15 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
     // rank order: value descending, then the later id first (the reverse of
     // the reference's ascending stable order)
     key[q] = has[q] ? (((uint64_t)tkey(sc[q]) << 32) | c) : 0ull;
-    if (has[q]) F.rkey[c] = key[q];
+    if (q < NS) F.rkey[c] = key[q];  // zero past n: never larger than a key
   }
-  if (lane < 4) F.rkey[n + (uint32_t)lane] = 0ull;
   lds_wait();
   // rank = number of candidates with a larger key
   uint32_t rk0 = 0, rk1 = 0;
   {
     const uint32_t nr = (n + 3u) & ~3u;
     uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-    if (n <= (uint32_t)kWave) {
+    if (NS == 1) {
       for (uint32_t j = 0; j < nr; j += 4) {
         a0 += F.rkey[j] > key[0] ? 1u : 0u;
         a1 += F.rkey[j + 1] > key[0] ? 1u : 0u;
@@ -517,7 +518,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
     }
     // cum(position) / sum is the reference's running sum after adding it
     const double c0 = dpp_scan_f64(wa[0]);
-    const double c1 = dpp_scan_f64(wa[1]) + rl_f64(c0, kWave - 1);
+    const double c1 = NS == 2 ? dpp_scan_f64(wa[1]) + rl_f64(c0, kWave - 1) : 0.0;
     const double lim = 1.0 - a.top_p_d;
     const double limS = lim * sum;
     const uint64_t rm0 = __ballot((uint32_t)lane < ns && c0 <= limS);
@@ -563,7 +564,7 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
 #pragma unroll
   for (int q = 0; q < 2; ++q) e[q] = live[q] ? w[q] : 0.0;
   const double acc0 = dpp_scan_f64(e[0]);
-  const double acc1 = dpp_scan_f64(e[1]) + rl_f64(acc0, kWave - 1);
+  const double acc1 = NS == 2 ? dpp_scan_f64(e[1]) + rl_f64(acc0, kWave - 1) : acc0;
   const double sum2 = rl_f64(acc1, kWave - 1);
   const double u = reinterpret_cast<const double*>(a.uniforms)[row];
   const double target = u * sum2;
@@ -654,6 +655,11 @@ __device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint3
       }
     }
   }
+}
+
+__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
+  if (n <= (uint32_t)kWave) idx_fast_finish_t<1>(a, row, n, L, F);
+  else idx_fast_finish_t<2>(a, row, n, L, F);
 }
 
 }  // namespace tc
