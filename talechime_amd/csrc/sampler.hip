@@ -684,47 +684,57 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       SeqSum<ITEMS> sq;
       sq.predict(ap, F.seq);
       lds_barrier();
-      sq.classify(ap, exm, force, e0, F.seq);
-      const float Sp = sq.total(F.seq);  // cross-lane: all lanes, before any divergence
       // Candidates, staged while the exact sum is finished.  The histogram of
       // per-thread maxima of d over ids not in the history puts the K-th largest
       // such d above -(b0 + 1) / 4; x' = d - L is monotone in d for those ids, so
       // every one whose x' can reach the K-th largest has d >= -(b0 + 1) / 4 less
       // a margin (2^-9, far above the roundings of d - L and the floats the
       // division by T can merge).  Ids in the history (x' * pen) are admitted
-      // against the same bound for every L the prediction allows.
+      // against the same bound for every L the prediction allows.  The
+      // thresholds come first (cross-lane, every lane active), so their LDS
+      // and DPP latency overlaps the classification.
+      const float Sp = sq.total(F.seq);
       const uint32_t cum = dpp_scan_u32(F.bins[lane_id()]);
       const uint64_t reach = __ballot(cum >= (uint32_t)a.K);
-      uint32_t sel = 0;
+      float thr_d = __builtin_inff(), thr_s = __builtin_inff();
       if (reach) {
         const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
-        const float thr_d = -(float)(b0 + 1u) * 0.25f - 0x1p-9f;
+        thr_d = -(float)(b0 + 1u) * 0.25f - 0x1p-9f;
         // an id in the history reaches the bound for some L in [L_lo, L_hi]
         // when (d - L_lo) * pen >= thr_d - L_hi, i.e. (pen > 0) d >= thr_s,
         // taken a margin far above its roundings lower
-        float thr_s = -__builtin_inff();
+        thr_s = -__builtin_inff();
         if (a.do_pen && a.pen_f > 0.0f) {
           const float tt = seq_tau(V);
           const float L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f, L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
           thr_s = L_lo + (thr_d - L_hi) / a.pen_f - 0x1p-9f;
         }
-        // one compare per element against the lower threshold; the few hits
-        // are then held to their own
-        const float thr_lo = thr_s < thr_d ? thr_s : thr_d;
+      }
+      sq.classify(ap, exm, force, e0, F.seq);
+      // one compare per element against the lower threshold; the few hits are
+      // then held to their own
+      uint32_t sel = 0;
+      const float thr_lo = thr_s < thr_d ? thr_s : thr_d;
 #pragma unroll
-        for (int i = 0; i < ITEMS; ++i) sel |= (d[i] >= thr_lo ? 1u : 0u) << i;
-        sel &= vm;
-        if (sel) {
+      for (int i = 0; i < ITEMS; ++i) sel |= (d[i] >= thr_lo ? 1u : 0u) << i;
+      sel &= vm;
+      if (sel) {
 #pragma unroll
-          for (int i = 0; i < ITEMS; ++i)
-            sel &= ~((d[i] >= (((seen >> i) & 1ull) ? thr_s : thr_d) ? 0u : 1u) << i);
-        }
+        for (int i = 0; i < ITEMS; ++i)
+          sel &= ~((d[i] >= (((seen >> i) & 1ull) ? thr_s : thr_d) ? 0u : 1u) << i);
       }
       const uint32_t c = (uint32_t)__builtin_popcount(sel);
       const uint32_t ci = dpp_scan_u32(c);
       if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
       lds_barrier();
-      const bool listed_ok = sq.write_list(ap, d, e0, F.seq);
+      uint32_t off, n;
+      wave_table_u32(F.wcand, &off, &n);
+      off += ci - c;
+      const bool stage = reach && n <= (uint32_t)FinLds::kCap;
+      // the list and the candidates in one pass over the elements
+      const bool listed_ok = sq.write_list(ap, d, e0, F.seq, stage ? sel : 0u, [&](int i) {
+        F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) | (uint32_t)(e0 + i);
+      });
       // the exception keys of glibc logf around the expected sum, in flight
       // while the sum is finished
       LogfKeys lk;
@@ -732,15 +742,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
         const float tt = seq_tau((int)sq.u_tot) + 0x1p-22f;
         logf_keys_index(lk, sq.p2_tot * (1.0f - tt), sq.p2_tot * (1.0f + tt));
       }
-      uint32_t off, n;
-      wave_table_u32(F.wcand, &off, &n);
-      off += ci - c;
-      if (reach && n <= (uint32_t)FinLds::kCap) {
-#pragma unroll
-        for (int i = 0; i < ITEMS; ++i)
-          if ((sel >> i) & 1u)
-            F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) |
-                                (uint32_t)(e0 + i);
+      if (stage) {
         lds_barrier();
         if (listed_ok) sq.replay_terms([](float v) { return expf_glibc_wave(v); }, F.seq);
         lds_barrier();
@@ -763,7 +765,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 #pragma unroll
           for (int i = 0; i < ITEMS; ++i) ex[i] = ((vm >> i) & 1u) ? expf_glibc(d[i]) : 0.0f;
           __syncthreads();
-          S = block_seqsum_slow<ITEMS>(ex, e0, V, F.seq.x, SeqFastLds::kCap, &F.seq.S);
+          S = block_seqsum_slow<ITEMS>(ex, e0, V, &F.seq.e[0].x, SeqFastLds::kCap, &F.seq.S);
         }
         if (wave_id() == 0) {
           const float L = logf_glibc_near(S, F.fref, F.lnref, F.invref, lk);

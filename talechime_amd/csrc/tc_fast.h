@@ -55,12 +55,17 @@ __device__ __forceinline__ void wave_table_f32(const float* tab, float* before, 
 // exp_approx keeps its terms within 4 ulps (2^-21 relative) of glibc's expf.
 constexpr float kSeqErr = 0x1p-21f;
 
+// A listed element, one 16-byte LDS store and load.
+struct alignas(16) ListEntry {
+  float x;        // its input (exact term not yet known) or its exact term
+  float P;        // the refined prediction of the running sum before it
+  uint32_t q;     // integer contributions of the safe elements before it (mod 2^32)
+  uint32_t info;  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: uncertainty count
+};
+
 struct SeqFastLds {
   static constexpr int kCap = 1024;
-  float x[kCap];      // listed element: its input (exact term not yet known) or its exact term
-  float P[kCap];      // the refined prediction of the running sum before it
-  uint32_t q[kCap];   // integer contributions of the safe elements before it (mod 2^32)
-  uint32_t info[kCap];  // bit 0: x is the exact term; bit 1: undecided (not a crossing); bits 8+: position
+  ListEntry e[kCap];
   float ua[kCap];     // the replay's walk: exact terms of the elements that stay listed,
   uint32_t uq[kCap];  // compacted inside each chunk of 64, and the integer
                       // contributions before each (less the earlier chunks' folds)
@@ -144,9 +149,16 @@ struct SeqSum {
   uint32_t c_tot, q_tot;
 
   __device__ __forceinline__ void predict(const float (&ap)[ITEMS], SeqFastLds& L) {
-    D = 0.0f;
+    // pairwise: a short dependent chain (any order of non-negative terms
+    // keeps the bound of ITEMS - 1 roundings)
+    float t[ITEMS];
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) D += ap[i];
+    for (int i = 0; i < ITEMS; ++i) t[i] = ap[i];
+#pragma unroll
+    for (int h = 1; h < ITEMS; h *= 2)
+#pragma unroll
+      for (int i = 0; i + h < ITEMS; i += 2 * h) t[i] += t[i + h];
+    D = t[0];
     const float inc = dpp_scan_f32(D);
     ex = dpp_prev_f32(inc);  // earlier lanes of this wave
     if (lane_id() == kWave - 1) L.wsum[wave_id()] = inc;
@@ -262,8 +274,12 @@ struct SeqSum {
     }
   }
 
+  // Also calls stage(i) for every element i whose bit is set in smask, in the
+  // same pass (a kernel's own per-element staging).  false: more than kCap
+  // listed (nothing listed is written; stage still runs).
+  template <class G>
   __device__ __forceinline__ bool write_list(const float (&ap)[ITEMS], const float (&x)[ITEMS], int pos0,
-                                             SeqFastLds& L) {
+                                             SeqFastLds& L, uint32_t smask, G stage) {
     uint32_t c_off, q_off;
     float p2, p2_all;
     wave_table_u32(L.wcnt, &c_off, &c_tot);
@@ -277,29 +293,33 @@ struct SeqSum {
     u_tot = (c_tot & 0xffffu) + (c_tot >> 16);
     c_tot &= 0xffffu;
     p2_tot = p2_all;
-    if (c_tot > (uint32_t)SeqFastLds::kCap) return false;
-    if (listed) {
+    const bool ok = c_tot <= (uint32_t)SeqFastLds::kCap;
+    const uint32_t lm = ok ? listed : 0u;
+    if (lm | smask) {
       uint32_t k = c_off, q = q_off;
       float P = P0, al = 0.0f;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
-        if ((listed >> i) & 1u) {
+        if ((lm >> i) & 1u) {
           const bool exa = (exact >> i) & 1u;
-          L.x[k] = exa ? ap[i] : x[i];
-          L.P[k] = p2 + (ulp0 != 0.0f ? (float)(q - q_off) * ulp0 + al : P - P0);
-          L.q[k] = q;
-          // bits 8+: the uncertainty count of the refined prediction
+          // bits 8+ of info: the uncertainty count of the refined prediction
           const uint32_t u = k + g + (ulp0 != 0.0f ? 0u : (uint32_t)i);
-          L.info[k] = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | (u << 8);
+          ListEntry en;
+          en.x = exa ? ap[i] : x[i];
+          en.P = p2 + (ulp0 != 0.0f ? (float)(q - q_off) * ulp0 + al : P - P0);
+          en.q = q;
+          en.info = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | (u << 8);
+          L.e[k] = en;
           ++k;
           al += ap[i];
         } else {
           q += r[i];
         }
+        if ((smask >> i) & 1u) stage(i);
         P = P + ap[i];
       }
     }
-    return true;
+    return ok;
   }
 
   // Every wave, chunks wave, wave + num_waves(), ... of 64 listed elements,
@@ -313,9 +333,18 @@ struct SeqSum {
     for (uint32_t c = wv; c * kWave < c_tot; c += nw) {
       const uint32_t k = c * kWave + (uint32_t)lane;
       const bool in = k < c_tot;
-      const uint32_t info = in ? L.info[k] : 1u;
-      const float xin = in ? L.x[k] : 0.0f;
-      const float Pk = in ? L.P[k] : 0.0f;
+      ListEntry en;
+      if (in) {
+        en = L.e[k];
+      } else {
+        en.x = 0.0f;
+        en.P = 0.0f;
+        en.q = 0u;
+        en.info = 1u;
+      }
+      const uint32_t info = en.info;
+      const float xin = en.x;
+      const float Pk = en.P;
       const float fx = f(xin);  // outside the select: f may need every lane
       const float a = (info & 1u) ? xin : fx;
       uint32_t rk = 0;
@@ -328,7 +357,7 @@ struct SeqSum {
       if (keep) {
         const uint32_t j = c * kWave + (uint32_t)__popcll(km & ((1ull << lane) - 1ull));
         L.ua[j] = a;
-        L.uq[j] = L.q[k] + (R - rs);
+        L.uq[j] = en.q + (R - rs);
       }
       if (lane == kWave - 1) {
         L.cf[c] = R;
