@@ -274,6 +274,37 @@ struct SeqSum {
     }
   }
 
+  // One pass over the elements: the list entries of the bits of lm (from
+  // position k0, integer sums from q0, refined prediction from p2) and
+  // stage(i) for the bits of smask.  SF: every lane of the wave in the short
+  // form (safe elements add r ulps of one binade; the others their terms).
+  template <bool SF, class G>
+  __device__ __forceinline__ void list_pass(const float (&ap)[ITEMS], const float (&x)[ITEMS], SeqFastLds& L,
+                                            uint32_t smask, G stage, uint32_t lm, uint32_t k0, uint32_t q0,
+                                            uint32_t g, float p2) const {
+    uint32_t k = k0, q = q0;
+    float acc = 0.0f;  // SF: the listed terms before; otherwise all terms before
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if ((lm >> i) & 1u) {
+        const bool exa = (exact >> i) & 1u;
+        ListEntry en;
+        en.x = exa ? ap[i] : x[i];
+        en.P = SF ? p2 + ((float)(q - q0) * ulp0 + acc) : p2 + acc;
+        en.q = q;
+        // bits 8+: the uncertainty count of the refined prediction
+        en.info = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | ((k + g + (SF ? 0u : (uint32_t)i)) << 8);
+        L.e[k] = en;
+        ++k;
+        if (SF) acc += ap[i];
+      } else {
+        q += r[i];
+      }
+      if (!SF) acc += ap[i];
+      if ((smask >> i) & 1u) stage(i);
+    }
+  }
+
   // Also calls stage(i) for every element i whose bit is set in smask, in the
   // same pass (a kernel's own per-element staging).  false: more than kCap
   // listed (nothing listed is written; stage still runs).
@@ -296,28 +327,12 @@ struct SeqSum {
     const bool ok = c_tot <= (uint32_t)SeqFastLds::kCap;
     const uint32_t lm = ok ? listed : 0u;
     if (lm | smask) {
-      uint32_t k = c_off, q = q_off;
-      float P = P0, al = 0.0f;
-#pragma unroll
-      for (int i = 0; i < ITEMS; ++i) {
-        if ((lm >> i) & 1u) {
-          const bool exa = (exact >> i) & 1u;
-          // bits 8+ of info: the uncertainty count of the refined prediction
-          const uint32_t u = k + g + (ulp0 != 0.0f ? 0u : (uint32_t)i);
-          ListEntry en;
-          en.x = exa ? ap[i] : x[i];
-          en.P = p2 + (ulp0 != 0.0f ? (float)(q - q_off) * ulp0 + al : P - P0);
-          en.q = q;
-          en.info = (exa ? 1u : 0u) | (((amb >> i) & 1u) << 1) | (u << 8);
-          L.e[k] = en;
-          ++k;
-          al += ap[i];
-        } else {
-          q += r[i];
-        }
-        if ((smask >> i) & 1u) stage(i);
-        P = P + ap[i];
-      }
+      // the short form is wave-uniform: one pass per form, each computing only
+      // its own refined prediction
+      if (__ballot(ulp0 == 0.0f) == 0ull)
+        list_pass<true>(ap, x, L, smask, stage, lm, c_off, q_off, g, p2);
+      else
+        list_pass<false>(ap, x, L, smask, stage, lm, c_off, q_off, g, p2);
     }
     return ok;
   }
