@@ -80,7 +80,7 @@ struct RowArgs {
   int exclude_id;
   int ras_win;
   float ras_thresh;  // (f32)win * tau
-  int fast;          // indextts: the streaming fast path applies (1 <= K <= 64 < V)
+  int fast;          // indextts, qwen: the streaming fast path applies (1 <= K <= 64 < V, sampling)
 };
 
 struct SurvLds {
@@ -188,9 +188,287 @@ __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
   }
 }
 
+// ================================================================ qwen, fast path
+// qwen semantics (sampling.rs:169-328 with the caller's penalty, masks and
+// EOS) for 1 <= K <= 64 < V on rows whose scores are finite or -inf:
+//  * the row, its history map and the transform, then the row max;
+//  * a 64-bucket histogram (quarter-unit wide) of the per-thread maxima below
+//    the row max bounds the K-th largest score from below, since K threads
+//    hold a score at or above the bucket where the count reaches K; every
+//    score at or above that bound (less a margin above the roundings of the
+//    bucket arithmetic) is a candidate, staged in vocabulary order (at most
+//    kQCand);
+//  * one wave finishes: ranks (value descending, id ascending: the general
+//    path's order), the top-k cut (ties kept), exp terms, and the reference's
+//    sequential f32 sums: the top-p denominator and running sum in rank order
+//    (255-299), then the softmax denominator and the CDF in vocabulary order
+//    (302-328), as readlane chains over at most kQCand lanes.
+// Anything else takes the general path below.
+constexpr int kQCand = 128;
+
+struct QFastLds {
+  uint32_t bits[kMaxVocabReg / 32];  // history ids present
+  uint32_t bins[64];
+  float wmax[kMaxWaves];
+  uint32_t wbad[kMaxWaves];
+  uint32_t wcand[kMaxWaves];
+  uint64_t cand[kQCand];  // (bits of the score << 32) | id, vocabulary order
+  uint64_t rkey[kQCand];
+  float er[kQCand];       // survivors' terms by rank
+  float vr[kQCand];       // and their scores
+};
+
+template <int NS>
+__device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, uint32_t n, float vmax, QFastLds& F) {
+  const int lane = lane_id();
+  float v[2];
+  uint32_t id[2];
+  bool has[2];
+  uint64_t key[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t c = (uint32_t)(q * kWave + lane);
+    has[q] = q < NS && c < n;
+    const uint64_t cv = has[q] ? F.cand[c] : 0ull;
+    v[q] = u2f((uint32_t)(cv >> 32));
+    id[q] = (uint32_t)cv;
+    key[q] = has[q] ? (((uint64_t)ckey(v[q]) << 32) | (uint64_t)(~c)) : 0ull;
+    if (q < NS) F.rkey[c] = key[q];
+  }
+  lds_wait();
+  uint32_t rk[2] = {0u, 0u};
+  {
+    const uint32_t nr = (n + 3u) & ~3u;
+    for (uint32_t j = 0; j < nr; j += 4) {
+      const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1], k2 = F.rkey[j + 2], k3 = F.rkey[j + 3];
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        rk[q] += ((k0 > key[q] ? 1u : 0u) + (k1 > key[q] ? 1u : 0u)) + ((k2 > key[q] ? 1u : 0u) + (k3 > key[q] ? 1u : 0u));
+    }
+  }
+  // top-k (224-249): keep v >= the K-th largest, ties kept
+  const uint32_t K = (uint32_t)a.K;
+  const uint64_t bk0 = __ballot(has[0] && rk[0] == K - 1u), bk1 = __ballot(has[1] && rk[1] == K - 1u);
+  const float kth = bk0 ? rl_f32(v[0], __builtin_ctzll(bk0)) : rl_f32(v[1], __builtin_ctzll(bk1));
+  bool surv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) surv[q] = has[q] && v[q] >= kth;
+  const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
+  const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  // softmax numerators over the survivors; the row max is the largest survivor
+  float e[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float t = q < NS ? expf_glibc_wave(surv[q] ? v[q] - vmax : 0.0f) : 0.0f;
+    e[q] = surv[q] ? t : 0.0f;
+  }
+  uint32_t flags = 0;
+  bool kept[2] = {surv[0], surv[1]};
+  if (a.do_topp) {
+    // top-p (255-299): survivors occupy ranks [0, ns)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (surv[q]) {
+        F.er[rk[q]] = e[q];
+        F.vr[rk[q]] = v[q];
+      }
+    lds_wait();
+    float er[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t r = (uint32_t)(q * kWave + lane);
+      er[q] = (q < NS && r < ns) ? F.er[r] : 0.0f;
+    }
+    float S = -0.0f;
+    for (uint32_t r = 0; r < ns; ++r) S += rl_f32(r < (uint32_t)kWave ? er[0] : er[1], (int)(r & 63u));
+    float pr[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) pr[q] = er[q] / S;
+    float cum = 0.0f;
+    uint32_t cut = ns;
+    for (uint32_t r = 0; r < ns; ++r) {
+      cum += rl_f32(r < (uint32_t)kWave ? pr[0] : pr[1], (int)(r & 63u));
+      if (cum > a.top_p_f) {
+        cut = r + 1u;
+        break;
+      }
+    }
+    if (cut < ns && F.vr[cut - 1u] == F.vr[cut]) flags |= TC_FLAG_TIE_CUT;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) kept[q] = surv[q] && rk[q] < cut;
+  }
+  // softmax + multinomial in vocabulary order (302-328): non-kept entries add +0
+  const uint64_t km0 = __ballot(kept[0]), km1 = __ballot(kept[1]);
+  float S2 = 0.0f;
+  for (uint64_t m = km0; m; m &= m - 1ull) S2 += rl_f32(e[0], __builtin_ctzll(m));
+  for (uint64_t m = km1; m; m &= m - 1ull) S2 += rl_f32(e[1], __builtin_ctzll(m));
+  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+  uint32_t tok = 0;
+  float pk[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) pk[q] = e[q] / S2;
+  if (u > 0.0f) {
+    float cum = 0.0f;
+    bool done = false;
+    for (uint64_t m = km0; m && !done; m &= m - 1ull) {
+      const int l = __builtin_ctzll(m);
+      cum += rl_f32(pk[0], l);
+      if (cum >= u) {
+        tok = rl_u32(id[0], l);
+        done = true;
+      }
+    }
+    for (uint64_t m = km1; m && !done; m &= m - 1ull) {
+      const int l = __builtin_ctzll(m);
+      cum += rl_f32(pk[1], l);
+      if (cum >= u) {
+        tok = rl_u32(id[1], l);
+        done = true;
+      }
+    }
+  }
+  if (lane == 0) {
+    a.out_ids[row] = tok;
+    if (a.out_status) a.out_status[row] = TC_OK;
+    if (a.out_flags) a.out_flags[row] = flags;
+    if (a.norm) a.norm[row] = S2;
+    if (a.topk_count) a.topk_count[row] = ns;
+    if (a.keep_count) a.keep_count[row] = (uint32_t)(__popcll(km0) + __popcll(km1));
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    if (a.topk_count && surv[q]) {
+      const uint32_t j = (q == 0 ? 0u : (uint32_t)__popcll(sm0)) + (uint32_t)__popcll((q == 0 ? sm0 : sm1) & below);
+      if (j < a.cap) a.topk_ids[(size_t)row * a.cap + j] = id[q];
+    }
+    if (a.keep_count && kept[q]) {
+      const uint32_t j = (q == 0 ? 0u : (uint32_t)__popcll(km0)) + (uint32_t)__popcll((q == 0 ? km0 : km1) & below);
+      if (j < a.cap) {
+        a.keep_ids[(size_t)row * a.cap + j] = id[q];
+        a.keep_probs[(size_t)row * a.cap + j] = pk[q];
+      }
+    }
+  }
+}
+
+// true: the row is sampled; false: every thread goes on to the general path
+// (the decision is the same in every thread).
+template <typename InT, int ITEMS>
+__device__ __forceinline__ bool qwen_fast(const RowArgs& a, QFastLds& F) {
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+  float x[ITEMS];
+  int shift;
+  load_row<ITEMS>(rp, V, x, &shift);
+  const bool use_seen = a.do_pen && a.hist_mode != TC_HIST_MASK;
+  constexpr int kHpt = 4;
+  uint32_t h0 = 0, h1 = 0;
+  if (use_seen) hist_range(a, row, &h0, &h1);
+  uint32_t hid[kHpt];
+#pragma unroll
+  for (int j = 0; j < kHpt; ++j) {
+    const uint32_t k = h0 + (uint32_t)t + (uint32_t)j * blockDim.x;
+    hid[j] = k < h1 ? a.hist_ids[k] : 0xffffffffu;
+  }
+  const int nwords = (V + 31) >> 5;
+  if (use_seen)
+    for (int w = t; w < nwords; w += blockDim.x) F.bits[w] = 0u;
+  if (t < 64) F.bins[t] = 0u;
+  lds_barrier();
+  if (use_seen) {
+#pragma unroll
+    for (int j = 0; j < kHpt; ++j)
+      if (hid[j] < (uint32_t)V) atomicOr(&F.bits[hid[j] >> 5], 1u << (hid[j] & 31u));
+    for (uint32_t k = h0 + (uint32_t)t + (uint32_t)kHpt * blockDim.x; k < h1; k += blockDim.x) {
+      const uint32_t hv = a.hist_ids[k];
+      if (hv < (uint32_t)V) atomicOr(&F.bits[hv >> 5], 1u << (hv & 31u));
+    }
+  }
+  lds_barrier();
+  const uint32_t vm = valid_mask<ITEMS>(V, shift);
+  const int e0 = t * ITEMS - shift;
+  uint64_t seen = 0;
+  if (use_seen) {
+    const int w0 = e0 >= 0 ? (e0 >> 5) : 0;
+    const uint32_t lo = w0 < nwords ? F.bits[w0] : 0u;
+    const uint32_t hi = w0 + 1 < nwords ? F.bits[w0 + 1] : 0u;
+    seen = ((((uint64_t)hi << 32) | lo) >> (e0 >= 0 ? (e0 & 31) : 0));
+    if (e0 < 0) seen <<= (uint32_t)(-e0);
+  }
+  // the caller chain (synthesis.rs:1238-1276) then temperature (sampling.rs:175-184)
+  float tmax = -__builtin_inff();
+  uint32_t bad = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    const int e = e0 + i;
+    float v = x[i];
+    if (a.do_pen) {
+      const bool pen = use_seen ? ((seen >> i) & 1ull) != 0ull : (a.pen_mask[e] > 0.0f);
+      if (pen) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
+    }
+    if (a.add_mask) v = v + a.add_mask[e];
+    if (e == a.eos_id) v = -__builtin_inff();
+    if (a.do_temp) v = v * a.tmul + 0.0f;
+    x[i] = v;
+    bad |= (__builtin_isnan(v) || v == __builtin_inff()) ? 1u : 0u;
+    tmax = v > tmax ? v : tmax;
+  }
+  {
+    const float wm = dpp_wave_max(tmax);
+    const uint32_t wb = dpp_wave_or(bad);
+    if (lane_id() == 0) {
+      F.wmax[wave_id()] = wm;
+      F.wbad[wave_id()] = wb;
+    }
+  }
+  lds_barrier();
+  const bool inw = lane_id() < num_waves();
+  const float vmax = dpp_wave_max(inw ? F.wmax[lane_id()] : -__builtin_inff());
+  const uint32_t any_bad = dpp_wave_or(inw ? F.wbad[lane_id()] : 0u);
+  if (any_bad || !(vmax > -__builtin_inff())) return false;
+  if (tmax >= vmax - 16.0f) {
+    const float db = (vmax - tmax) * 4.0f;
+    if (db < 64.0f) atomicAdd(&F.bins[(uint32_t)db], 1u);
+  }
+  lds_barrier();
+  const uint32_t cum = dpp_scan_u32(F.bins[lane_id()]);
+  const uint64_t reach = __ballot(cum >= (uint32_t)a.K);
+  if (!reach) return false;
+  const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
+  const float thr = vmax - ((float)(b0 + 1u) * 0.25f + (0x1p-16f + __builtin_fabsf(vmax) * 0x1p-20f));
+  uint32_t sel = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) sel |= (x[i] >= thr ? 1u : 0u) << i;
+  sel &= vm;
+  const uint32_t c = (uint32_t)__builtin_popcount(sel);
+  const uint32_t ci = dpp_scan_u32(c);
+  if (lane_id() == kWave - 1) F.wcand[wave_id()] = ci;
+  lds_barrier();
+  uint32_t off, n;
+  wave_table_u32(F.wcand, &off, &n);
+  if (n > (uint32_t)kQCand) return false;
+  off += ci - c;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((sel >> i) & 1u) F.cand[off++] = ((uint64_t)f2u(x[i]) << 32) | (uint32_t)(e0 + i);
+  lds_barrier();
+  if (wave_id() == 0) {
+    if (n <= (uint32_t)kWave) qwen_fast_finish_t<1>(a, row, n, vmax, F);
+    else qwen_fast_finish_t<2>(a, row, n, vmax, F);
+  }
+  return true;
+}
+
 // ================================================================ qwen
 template <typename InT, int ITEMS>
 __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
+  if (a.fast) {
+    __shared__ QFastLds qf;
+    if (qwen_fast<InT, ITEMS>(a, qf)) return;
+    __syncthreads();
+  }
   __shared__ uint8_t s_seen[kMaxVocabReg];
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
@@ -1814,6 +2092,7 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
       a.K = p->top_k > 0 ? (int)(p->top_k < vocab ? p->top_k : vocab) : 0;
       a.do_topp = p->top_p < 1.0 && p->top_p > 0.0;
       a.top_p_f = (float)p->top_p;
+      a.fast = !a.greedy && a.K >= 1 && a.K <= 64 && a.K < V;
       break;
     }
     case TC_COSY_RAS: {  // llm.rs:436-445
