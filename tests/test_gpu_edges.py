@@ -138,6 +138,29 @@ def test_qwen_reference_rows(sampler):
     assert g["keep_ids"][0, :2].tolist() == [500, 1001]
 
 
+def test_qwen_fast_path_and_fallback_distributions(sampler):
+    """Rows the qwen fast path stages (peaked scores) and rows it hands to the
+    general path (flat scores: more than 128 candidates near the k-th; -inf
+    entries; k above 64), each bit-exact against the oracle with the
+    verification outputs."""
+    g_ = np.random.default_rng(77)
+    for V in (2048, 3072):
+        rows = []
+        for sigma in (0.05, 0.5, 2.0, 6.0, 20.0):
+            rows.append((g_.standard_normal(V) * sigma).astype(np.float32))
+        masked = (g_.standard_normal(V) * 3).astype(np.float32)
+        masked[g_.integers(0, V, V // 3)] = NEG
+        rows.append(masked)
+        x = np.stack(rows)
+        n = len(rows)
+        hist = [g_.integers(0, V, 80).tolist() for _ in range(n)]
+        u = [O.QwenRng(V + r).rand_f32() for r in range(n)]
+        for k, p in ((1, 0.9), (2, 0.5), (50, 0.8), (64, 1.0), (65, 0.9), (200, 0.7)):
+            g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.9, top_k=k, top_p=p, penalty=1.2)
+            tie = (o["flags"] & 1) != 0
+            same(g, o, rows=[r for r in range(n) if not tie[r]])
+
+
 def test_qwen_ties_and_degenerate_rows(sampler):
     rows = [
         np.zeros(64, np.float32),                     # all equal: ties at top-k and top-p
