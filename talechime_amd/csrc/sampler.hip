@@ -188,6 +188,103 @@ __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
   }
 }
 
+// ================================================================ qwen, many survivors
+// No top-p and more survivors than the LDS stage holds (top-k off or wide):
+// softmax over the survivors and the multinomial draw (sampling.rs:302-328)
+// over the register-resident row.  The denominator is the reference's
+// sequential f32 sum in vocabulary order of the exact terms (non-survivors
+// add +0), and the CDF its running sums of e / S2 (block_seqsum, seq_prefix);
+// the first index whose running sum reaches u is the token (0 when u <= 0 or
+// none does).  Verification outputs: the first `cap` survivors in vocabulary
+// order with their probabilities.
+template <int ITEMS>
+__device__ __forceinline__ void qwen_wide_cdf(const RowArgs& a, const float (&x)[ITEMS], uint32_t surv, uint32_t vm,
+                                              int e0, uint32_t n, uint32_t flags, SurvLds& sv, BlockScratch& s,
+                                              SeqLds& sq, ScanLds& sc) {
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  float* stage = reinterpret_cast<float*>(&sv);  // the survivor stage is not in use here
+  constexpr int kStage = (int)(sizeof(SurvLds) / sizeof(float));
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((surv >> i) & 1u) m = rmaxf(m, x[i]);
+  const float vmax = block_max(m, s);
+  float ev[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) ev[i] = ((surv >> i) & 1u) ? expf_glibc(x[i] - vmax) : 0.0f;
+  auto same = [](float v) { return v; };
+  float S2;
+  {
+    SeqThread<ITEMS> th;
+    if (!block_seqsum<ITEMS>(ev, ~0u, ev, same, e0, 0, th, sq, sc, &S2))
+      S2 = block_seqsum_slow<ITEMS>(ev, e0, V, stage, kStage, &sq.S);
+  }
+  float pv[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) pv[i] = ((surv >> i) & 1u) ? ev[i] / S2 : 0.0f;
+  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+  uint32_t tok = 0;
+  if (u > 0.0f) {
+    uint32_t found = 0xffffffffu;
+    SeqThread<ITEMS> th;
+    float Sp;
+    if (block_seqsum<ITEMS>(pv, ~0u, pv, same, e0, 0, th, sq, sc, &Sp)) {
+      float pre[ITEMS];
+      seq_prefix<ITEMS>(th, sq, pre);
+      uint32_t first = 0xffffffffu;
+#pragma unroll
+      for (int i = ITEMS - 1; i >= 0; --i)
+        if (((vm >> i) & 1u) && pre[i] >= u) first = (uint32_t)(e0 + i);
+      found = block_min_u(first, s);
+    } else {
+      // one lane walks the staged probabilities a chunk at a time
+      __shared__ uint32_t s_found;
+      float acc = 0.0f;
+      for (int c0 = 0; c0 < V; c0 += kStage) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+          const int e = e0 + i;
+          if (((vm >> i) & 1u) && e >= c0 && e < c0 + kStage) stage[e - c0] = pv[i];
+        }
+        __syncthreads();
+        if (t == 0) {
+          const int c1 = (c0 + kStage < V) ? c0 + kStage : V;
+          for (int e = c0; e < c1 && found == 0xffffffffu; ++e) {
+            acc += stage[e - c0];
+            if (acc >= u) found = (uint32_t)e;
+          }
+          s_found = found;
+        }
+        __syncthreads();
+        found = s_found;
+        __syncthreads();
+        if (found != 0xffffffffu) break;
+      }
+    }
+    tok = found != 0xffffffffu ? found : 0u;
+  }
+  finish_row(a, row, tok, TC_OK, flags);
+  put_norm(a, row, S2);
+  if (a.topk_count || a.keep_count) {
+    uint32_t tot;
+    const uint32_t pos0 = block_excl_scan((uint32_t)__builtin_popcount(surv), s, &tot);
+    uint32_t p = pos0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((surv >> i) & 1u) {
+        if (p < a.cap) {
+          if (a.topk_count) a.topk_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
+          if (a.keep_count) {
+            a.keep_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
+            a.keep_probs[(size_t)row * a.cap + p] = pv[i];
+          }
+        }
+        ++p;
+      }
+    if (t == 0 && a.keep_count) a.keep_count[row] = n;
+  }
+}
+
 // ================================================================ qwen, fast path
 // qwen semantics (sampling.rs:169-328 with the caller's penalty, masks and
 // EOS) for 1 <= K <= 64 < V on rows whose scores are finite or -inf:
@@ -474,6 +571,8 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
   __shared__ uint32_t s_hist[256];
   __shared__ BlockScratch s;
   __shared__ uint32_t s_out[4];
+  __shared__ SeqLds qsq;
+  __shared__ ScanLds qsc;
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
   float x[ITEMS];
@@ -559,6 +658,11 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
   const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
   write_topk(a, row, sv, n);
   if (n > (uint32_t)kSurvCap) {
+    if (!a.do_topp) {
+      qwen_wide_cdf<ITEMS>(a, x, surv, vm, e0, n, flags, sv, s, qsq, qsc);
+      return;
+    }
+    // top-p over more survivors than the LDS stage holds: not handled
     finish_row(a, row, 0u, TC_EUNSUPPORTED, flags);
     if (t == 0 && a.keep_count) a.keep_count[row] = 0;
     put_norm(a, row, __builtin_nanf(""));

@@ -161,6 +161,27 @@ def test_qwen_fast_path_and_fallback_distributions(sampler):
             same(g, o, rows=[r for r in range(n) if not tie[r]])
 
 
+def test_qwen_many_survivors_without_top_p(sampler):
+    """top-k off (or wider than 1024) and top-p off: softmax and CDF over every
+    survivor of the register-resident row, bit-exact with the verification
+    outputs; top-p over that many survivors still reports TC_EUNSUPPORTED."""
+    g_ = np.random.default_rng(31)
+    for V in (3072, 8194, 16000):
+        x = (g_.standard_normal((6, V)) * 2).astype(np.float32)
+        x[1, g_.integers(0, V, V // 4)] = NEG
+        x[2, :] = 0.0                                    # every probability equal
+        x[3, : V // 2] = NEG
+        hist = [g_.integers(0, V, 64).tolist() for _ in range(6)]
+        u = [0.0, 0.25, 0.5, 0.999999, 1.0, O.QwenRng(V).rand_f32()]
+        for k in (0, 5000, V + 3):
+            g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.8, top_k=k, top_p=1.0, penalty=1.1)
+            same(g, o)
+        g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.8, top_k=0, top_p=0.9, penalty=1.1)
+        wide = o["topk_count"] > KSURV
+        assert (g["status"][wide] == _lib.TC_EUNSUPPORTED).all()
+        same(g, o, rows=np.nonzero(~wide)[0])
+
+
 def test_qwen_ties_and_degenerate_rows(sampler):
     rows = [
         np.zeros(64, np.float32),                     # all equal: ties at top-k and top-p
