@@ -457,6 +457,7 @@ struct FinLds {
   uint64_t cand[kCap];      // (bits of d, history bit 31 | id) in vocabulary order
   uint64_t rkey[kCap + 4];  // rank keys, zero padded
   double wr[kCap];          // top-p weights by ascending position (rank ns-1-p)
+  float wr32[kCap];         // the same in f32 (the first, f32 decisions)
 };
 
 // One-wave finish of an indextts row from its n (K <= n <= 128) candidates
@@ -540,6 +541,99 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   for (int q = 0; q < 2; ++q) surv[q] = has[q] && !(sc[q] < kth);
   const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
   const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  // ---- f32 decisions first (when no verification outputs are asked for):
+  // weights exp(x'' - max) by exp_approx, within 2.5 ulps of the reference's
+  // f64 values (below 2^-87 they are taken as 0: under 2^-125 of the sum),
+  // f32 tree sums and scans.  (ns + 32) * 2^-21 of a sum bounds the f32
+  // weights, sums and scans and the reference's f64 sequential normalised
+  // sums together; a decision inside that margin goes to the f64 path below.
+  if (!a.topk_count) {
+    float w32[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float dq = sc[q] - vmax;
+      w32[q] = (surv[q] && dq >= -87.0f) ? exp_approx(dq) : 0.0f;
+    }
+    bool ok = true;
+    uint32_t rc = ns;
+    if (a.do_topp) {
+      const float sum32 = dpp_wave_sum(w32[0] + w32[1]);
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        if (surv[q]) F.wr32[ns - 1u - rk[q]] = w32[q];
+      lds_wait();
+      float wa[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t ap = (uint32_t)(q * kWave + lane);
+        wa[q] = (q < NS && ap < ns) ? F.wr32[ap] : 0.0f;
+      }
+      const float c0 = dpp_scan_f32(wa[0]);
+      const float c1 = NS == 2 ? dpp_scan_f32(wa[1]) + rl_f32(c0, kWave - 1) : 0.0f;
+      const float limS = (float)(1.0 - a.top_p_d) * sum32;
+      const uint64_t rm0 = __ballot((uint32_t)lane < ns && c0 <= limS);
+      const uint64_t rm1 = __ballot((uint32_t)(kWave + lane) < ns && c1 <= limS);
+      const uint32_t n_rm = (uint32_t)(__popcll(rm0) + __popcll(rm1));
+      rc = ns - n_rm;
+      const float mg = (float)(ns + 32u) * 0x1p-21f * sum32;
+      bool close = false;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t ap = (uint32_t)(q * kWave + lane);
+        const float cq = q == 0 ? c0 : c1;
+        close = close || (ap < ns && (ap + 1u == n_rm || ap == n_rm) && __builtin_fabsf(cq - limS) <= mg);
+      }
+      ok = __ballot(close) == 0ull;
+    }
+    if (ok) {
+      const uint32_t live_r = rc > (uint32_t)a.min_keep ? rc : (uint32_t)a.min_keep;
+      bool lv[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) lv[q] = surv[q] && rk[q] < live_r;
+      const uint64_t lm0 = __ballot(lv[0]), lm1 = __ballot(lv[1]);
+      const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
+      float e32[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) e32[q] = lv[q] ? w32[q] : 0.0f;
+      const float acc0 = dpp_scan_f32(e32[0]);
+      const float acc1 = NS == 2 ? dpp_scan_f32(e32[1]) + rl_f32(acc0, kWave - 1) : acc0;
+      const float sum2 = rl_f32(acc1, kWave - 1);
+      const float target = (float)reinterpret_cast<const double*>(a.uniforms)[row] * sum2;
+      const uint64_t pz0 = __ballot(lv[0] && e32[0] > 0.0f), pz1 = __ballot(lv[1] && e32[1] > 0.0f);
+      const uint64_t hit0 = __ballot(lv[0] && e32[0] > 0.0f && acc0 > target);
+      const uint64_t hit1 = __ballot(lv[1] && e32[1] > 0.0f && acc1 > target);
+      ok = nl != 0u && (pz0 | pz1) != 0ull;
+      uint32_t pick = 0;
+      bool found = true;
+      if (hit0) pick = (uint32_t)__builtin_ctzll(hit0);
+      else if (hit1) pick = 64u + (uint32_t)__builtin_ctzll(hit1);
+      else {
+        found = false;
+        pick = pz1 ? 64u + 63u - (uint32_t)__builtin_clzll(pz1) : (pz0 ? 63u - (uint32_t)__builtin_clzll(pz0) : 0u);
+      }
+      const float mg2 = (float)(nl + 32u) * 0x1p-21f * sum2;
+      const float a_pick = rl_f32(pick < 64 ? acc0 : acc1, (int)(pick & 63u));
+      bool close = __builtin_fabsf(a_pick - target) <= mg2;
+      if (found) {
+        const uint64_t below0 = pick < 64 ? (pz0 & ((1ull << pick) - 1ull)) : pz0;
+        const uint64_t below1 = pick < 64 ? 0ull : (pz1 & ((1ull << (pick - 64u)) - 1ull));
+        if (below1 || below0) {
+          const uint32_t prev = below1 ? 64u + 63u - (uint32_t)__builtin_clzll(below1) : 63u - (uint32_t)__builtin_clzll(below0);
+          const float a_prev = rl_f32(prev < 64 ? acc0 : acc1, (int)(prev & 63u));
+          close = close || __builtin_fabsf(a_prev - target) <= mg2;
+        }
+      }
+      if (ok && !close) {
+        const uint32_t tok = rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u));
+        if (lane == 0) {
+          a.out_ids[row] = tok;
+          if (a.out_status) a.out_status[row] = TC_OK;
+          if (a.out_flags) a.out_flags[row] = 0u;
+        }
+        return;
+      }
+    }
+  }
   // f64 weights (generation.rs:108-116 for top-p, 289-293 for the draw)
   const double mxd = (double)vmax;
   double w[2];
