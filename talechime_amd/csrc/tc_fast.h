@@ -398,7 +398,49 @@ struct SeqSum {
     uint32_t qp = 0, bad = 0, xb = 0, fold = 0;
     bool pos = false;  // a positive term or a nonzero d seen in an earlier chunk
     const uint32_t nch = (c_tot + kWave - 1) / kWave;
-    for (uint32_t c = 0; c < nch; ++c) {
+    // Several chunks whose kept elements fit one wave are gathered into one
+    // (lane j: kept element j, its integer sum with the folds of the chunks
+    // before its own) and walked once.
+    bool gather = false;
+    if (nch > 1u) {
+      const bool lc = (uint32_t)lane < nch;
+      const uint32_t ckl = lc ? L.ck[lane] : 0u, cfl = lc ? L.cf[lane] : 0u;
+      const uint32_t cki = dpp_scan_u32(ckl), cfi = dpp_scan_u32(cfl);
+      const uint32_t kept = rl_u32(cki, kWave - 1);
+      gather = kept <= (uint32_t)kWave;
+      if (gather) {
+        uint32_t src = 0, fadd = 0;
+        for (uint32_t c = 0; c < nch; ++c) {
+          const uint32_t n_c = rl_u32(ckl, (int)c), b = rl_u32(cki, (int)c) - n_c, f = rl_u32(cfi, (int)c) - rl_u32(cfl, (int)c);
+          if ((uint32_t)lane >= b && (uint32_t)lane < b + n_c) {
+            src = c * kWave + ((uint32_t)lane - b);
+            fadd = f;
+          }
+        }
+        const bool in = (uint32_t)lane < kept;
+        const uint32_t qk = in ? L.uq[src] + fadd : 0u;
+        const uint32_t qprev = dpp_prev_u32(qk);
+        const uint32_t dv = in ? qk - qprev : 0u;
+        const float av = in ? L.ua[src] : 0.0f;
+        qp = kept ? rl_u32(qk, (int)kept - 1) : 0u;
+        fold = rl_u32(cfi, kWave - 1);  // the folds of every chunk
+        const uint64_t md = __ballot(dv != 0u), ma = __ballot(av > 0.0f);
+        if (md != 0ull && (ma & ((md & (0ull - md)) - 1ull)) == 0ull) bad = 1u;
+#pragma unroll
+        for (int g = 0; g < kWave / 16; ++g) {
+          if ((uint32_t)(g * 16) >= kept) break;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const uint32_t di = rl_u32(dv, g * 16 + i);
+            const float ai = rl_f32(av, g * 16 + i);
+            const uint32_t sb = f2u(s), sb2 = sb + di;
+            xb = max(xb, sb ^ sb2);
+            s = u2f(sb2) + ai;
+          }
+        }
+      }
+    }
+    for (uint32_t c = 0; c < (gather ? 0u : nch); ++c) {
       const uint32_t nu = (uint32_t)__builtin_amdgcn_readfirstlane((int)L.ck[c]);
       const uint32_t cfc = (uint32_t)__builtin_amdgcn_readfirstlane((int)L.cf[c]);
       if (nu == 0u) {
