@@ -3,12 +3,18 @@
 //
 // One workgroup samples one row.  The row is streamed from HBM once with
 // 16-byte loads and stays in registers (ITEMS consecutive elements per
-// thread); the history ids become a byte map in LDS; the top-k threshold is a
-// four-pass radix select over 32-bit order keys with LDS histograms; the
-// survivors are compacted into LDS in vocabulary order with a block scan; the
-// order-dependent steps (the reference's sequential f32/f64 sums, cumulative
-// cut-offs and inverse-CDF walks) run over the survivors in exactly the
-// reference's order.
+// thread); the history ids become a bit or byte map in LDS.
+//  * Fast paths (indextts and qwen with 1 <= top_k <= 64): a histogram of the
+//    per-thread maxima bounds the k-th score, the few candidates above it are
+//    staged in LDS, and one wave finishes the row (ranks by counting, the
+//    reference's order-dependent sums as wave scans or readlane chains).  The
+//    indextts log_softmax denominator is the reference's sequential f32 sum,
+//    reproduced exactly (tc_fast.h).
+//  * General paths: the top-k threshold is a four-pass radix select over
+//    32-bit order keys with LDS histograms; the survivors are compacted into
+//    LDS in vocabulary order with a block scan; the order-dependent steps (the
+//    reference's sequential f32/f64 sums, cumulative cut-offs and inverse-CDF
+//    walks) run over the survivors in exactly the reference's order.
 //
 // Variants and the reference code each kernel follows (talechime repository):
 //   k_qwen      crates/qwen3-tts/src/generation/sampling.rs:169-219, 224-328, 334-395,
@@ -1814,7 +1820,6 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_nano(RowArgs a) {
   __shared__ SurvLds sv;
   __shared__ uint32_t s_hist[256];
   __shared__ BlockScratch s;
-  __shared__ uint32_t s_out[4];
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
   float x[ITEMS];

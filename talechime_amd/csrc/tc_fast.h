@@ -1,9 +1,9 @@
 // tc_fast.h -- the streaming fast path of the indextts sampler: an LDS-only
 // barrier, an exact emulation of a sequential f32 sum classified in f32
-// arithmetic, and a one-wave finish whose order-dependent f64 sums are wave
-// scans with a rigorous error margin, falling back to the reference's
-// sequential loops when a decision lies inside that margin.  Cross-lane
-// traffic uses DPP (tc_dpp.h).
+// arithmetic (SeqSum), and a one-wave finish whose order-dependent sums are
+// wave scans checked against a rigorous error margin: f32 first, then f64,
+// then the reference's sequential loops when a decision lies inside the f64
+// margin.  Cross-lane traffic uses DPP (tc_dpp.h).
 #pragma once
 
 #include "tc_device.h"
@@ -49,7 +49,7 @@ __device__ __forceinline__ void wave_table_f32(const float* tab, float* before, 
 // after provably stays in one binade [2^e, 2^(e+1)) adds round(t / 2^(e-23))
 // ulps, an integer; when the approximate term cannot settle that rounding
 // the exact term is computed.  Ties, binade crossings and the first positive
-// term go to a list that one wave replays exactly.  The integer
+// term go to a list that is replayed exactly.  The integer
 // contributions are summed modulo 2^32: between two listed elements they stay
 // inside one binade, so every difference the replay takes is below 2^24.
 // exp_approx keeps its terms within 4 ulps (2^-21 relative) of glibc's expf.
