@@ -19,6 +19,8 @@
  *                            (log_softmax, apply_repetition_penalty, apply_temperature,
  *                            apply_top_k, apply_top_p) then sample_without_replacement
  *                            (generation.rs:280) with one draw per row
+ *   tc_indextts_beam_step    crates/indextts/src/generation.rs:640-701, the joint scores
+ *                            and sample_without_replacement of the beam-sample loop
  *   tc_sample (TC_MOSS)      crates/moss-tts/src/sampling.rs:22 `sample`
  *   tc_sample (TC_MOSS_NANO) crates/moss-tts/src/nano/sampling.rs:11 `Sampler::sample`
  *   tc_apply_repetition_penalty            sampling.rs:334
@@ -27,6 +29,7 @@
  *   tc_build_suppression_mask              crates/qwen3-tts/src/generation/tts.rs:22
  *   tc_apply_token_suppression_with_mask   tts.rs:44
  *   tc_update_penalty_mask                 crates/qwen3-tts/src/synthesis.rs:568
+ *                                          (also fused into tc_sample: d_mark_mask)
  */
 #ifndef TALECHIME_HIP_H
 #define TALECHIME_HIP_H
@@ -38,7 +41,7 @@
 extern "C" {
 #endif
 
-#define TC_ABI_VERSION 1
+#define TC_ABI_VERSION 2
 
 typedef struct tc_ctx tc_ctx;
 typedef void* tc_stream; /* a hipStream_t */
@@ -105,6 +108,11 @@ typedef struct tc_sample_params {
   int32_t exclude_id;       /* moss: forced to -inf; -1 = none */
   const float* d_add_mask;  /* qwen: additive [V] mask (suppression), or NULL */
   const float* d_pen_mask;  /* qwen: [V] penalty mask for TC_HIST_MASK */
+  float* d_mark_mask;       /* optional [V] f32: each row sampled with TC_OK sets
+                               d_mark_mask[id] = 1.0 (synthesis.rs:568-579
+                               update_penalty_mask fused into the step; ids >= V are
+                               ignored).  May equal d_pen_mask only when rows == 1:
+                               the row reads the mask before it marks it.  NULL = off */
 } tc_sample_params;
 
 /* Optional verification outputs (device pointers; pass NULL to skip).  Ids are
@@ -144,6 +152,38 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* params, const void* d_logits,
               const uint32_t* d_hist_ids, const void* d_uniforms, uint32_t* d_out_ids,
               int32_t* d_out_status, uint32_t* d_out_flags, const tc_verify_out* verify,
               tc_stream stream);
+
+/*
+ * One indextts beam-sample step (crates/indextts/src/generation.rs:640-701 after the
+ * logits: the processors of each beam row (643-662), the joint beam-major scores
+ * score + beam score in f64 (663-664), sample_without_replacement with n_draws
+ * draws per batch element (680, 280-303), candidates sorted by score descending,
+ * stable (690)).  Replaces the `joint` / `candidates` computation of that loop;
+ * BeamSearchScorer::process (generation.rs:386-440) consumes the candidates.
+ *   d_logits      [batch * num_beams, ld]; row bi * num_beams + j is beam j of element bi
+ *   d_hist_off/ids CSR histories per row (the beam's input ids), as tc_sample
+ *   d_beam_scores [batch * num_beams] f64 running beam scores
+ *   d_uniforms    [batch * n_draws] f64, element bi's draws at bi * n_draws (the
+ *                 reference's rng.random::<f64>() calls in order); n_draws is
+ *                 2 * num_beams in the reference (generation.rs:620), at most 64
+ *   d_cand_flat   [batch * n_draws] u32 flat index beam * vocab + id
+ *   d_cand_scores [batch * n_draws] f64 joint scores, descending
+ *   d_out_status  [batch] i32: TC_ETOOFEW when fewer than n_draws joint scores are
+ *                 finite (generation.rs:284-286); d_out_flags [batch] (may be NULL):
+ *                 TC_FLAG_NEAR_TIE when a top-p or draw decision lay within the f64
+ *                 exp error of the reference's libm
+ * num_beams <= 64, num_beams * vocab < 2^32, batch * num_beams <= the context's
+ * max_rows; at most 1024 kept ids per row and 4096 per element (else
+ * TC_EUNSUPPORTED in d_out_status).  The context's first beam step allocates its
+ * row-pass workspace (16 KiB per max_rows row): make one call before capturing
+ * a graph.  params->variant must be TC_INDEXTTS; d_mark_mask is ignored.
+ */
+int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* params, const void* d_logits, int dtype,
+                          size_t batch, size_t num_beams, size_t vocab, size_t ld,
+                          const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+                          const double* d_beam_scores, const double* d_uniforms, size_t n_draws,
+                          uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
+                          uint32_t* d_out_flags, tc_stream stream);
 
 /* qwen building blocks on f32 [rows, ld] (d_in may equal d_out).
  * tc_apply_repetition_penalty builds its [V] mask in the context's workspace. */

@@ -108,6 +108,9 @@ def lib():
         L.tco_idx_sample_wo_replacement.restype = C.c_int
         L.tco_idx_sample_wo_replacement.argtypes = [C.POINTER(C.c_double), sz, sz,
                                                     C.POINTER(C.c_double), C.POINTER(sz)]
+        vp = C.c_void_p
+        L.tco_idx_beam_step.restype = C.c_int
+        L.tco_idx_beam_step.argtypes = [C.POINTER(Params), vp, sz, sz, sz, vp, vp, vp, vp, sz, vp, vp, vp]
         L.tco_cosy_nucleus.restype = C.c_uint32
         L.tco_cosy_nucleus.argtypes = [f32p, sz, C.c_float, sz, C.c_float, C.POINTER(C.c_int),
                                        u32p, f32p, u32p]
@@ -279,6 +282,33 @@ def idx_sample_wo_replacement(scores, n, uniforms):
     if st != OK:
         return None
     return [int(out[i]) for i in range(n)]
+
+
+def idx_beam_step(params, logits, hist_off, hist_ids, beam_scores, num_beams, uniforms, n_draws):
+    """One indextts beam-sample step (generation.rs:640-701).  Returns a dict:
+    flat [batch, n_draws] (beam * V + id, by score descending), scores (f64),
+    status [batch]."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    rows, V = logits.shape
+    assert rows % num_beams == 0
+    batch = rows // num_beams
+    ho = None if hist_off is None else np.ascontiguousarray(hist_off, np.uint32)
+    hi = None if hist_ids is None else np.ascontiguousarray(hist_ids, np.uint32)
+    if hi is not None and hi.size == 0:
+        hi = np.zeros(1, np.uint32)
+    bs = np.ascontiguousarray(beam_scores, np.float64)
+    un = np.ascontiguousarray(uniforms, np.float64)
+    assert bs.size >= rows and un.size >= batch * n_draws
+    flat = np.zeros((batch, n_draws), np.uint32)
+    sc = np.zeros((batch, n_draws), np.float64)
+    st = np.zeros(batch, np.int32)
+    rc = lib().tco_idx_beam_step(C.byref(params), logits.ctypes.data, batch, num_beams, V,
+                                 None if ho is None else ho.ctypes.data, None if hi is None else hi.ctypes.data,
+                                 bs.ctypes.data, un.ctypes.data, n_draws, flat.ctypes.data, sc.ctypes.data,
+                                 st.ctypes.data)
+    if rc != OK:
+        raise ValueError(f"tco_idx_beam_step: status {rc}")
+    return {"flat": flat, "scores": sc, "status": st}
 
 
 def cosy_nucleus(probs, top_p, top_k, u0):

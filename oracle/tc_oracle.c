@@ -703,10 +703,9 @@ static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const u
 
 /* indextts: generation.rs:643-666 for one row with beam score 0, then
  * sample_without_replacement with n = 1 (generation.rs:280-303). */
-static int row_indextts(const tco_params* p, float* x, size_t V, size_t row, const uint32_t* ids,
-                        size_t n_ids, double u, uint32_t* tok, uint32_t* flags, row_verify* rv) {
-  (void)flags;
-  (void)row;
+/* The processors of one row, in place (generation.rs:643-662, sampling on). */
+static void idx_process_row(const tco_params* p, float* x, size_t V, const uint32_t* ids, size_t n_ids,
+                            row_verify* rv) {
   {
     float ls = idx_log_softmax_ls(x, V);
     if (rv) rv->norm = ls;
@@ -717,6 +716,13 @@ static int row_indextts(const tco_params* p, float* x, size_t V, size_t row, con
   if (p->top_k != 0) tco_idx_top_k(x, V, p->top_k, p->min_keep);
   rv_set_topk_from_row(rv, x, V);
   if (p->top_p < 1.0) tco_idx_top_p(x, V, p->top_p, p->min_keep);
+}
+
+static int row_indextts(const tco_params* p, float* x, size_t V, size_t row, const uint32_t* ids,
+                        size_t n_ids, double u, uint32_t* tok, uint32_t* flags, row_verify* rv) {
+  (void)flags;
+  (void)row;
+  idx_process_row(p, x, V, ids, n_ids, rv);
   double* joint = (double*)malloc((V ? V : 1) * sizeof(double));
   for (size_t i = 0; i < V; i++) joint[i] = (double)x[i] + 0.0;
   size_t pick = 0;
@@ -939,6 +945,58 @@ static void sample_one_row(const tco_params* p, const float* logits, size_t r, s
     if (!ver->keep_probs) free(rv->keep_p);
   }
   free(x);
+}
+
+/* One beam-sample step of indextts (generation.rs:640-701) for `batch`
+ * elements of `nb` beam rows each (row bi * nb + j is beam j of element bi):
+ * each row's processors (643-662), the joint beam-major scores with the row's
+ * running beam score added, score as f64 + bonus (663-664), then per element
+ * sample_without_replacement with n_draws draws (680; the uniforms of element
+ * bi are uniforms[bi * n_draws ..]) and the candidates (joint score, flat
+ * index j * V + id) sorted by score descending, stable (690).  status[bi] is
+ * TCO_ETOOFEW when the element has fewer than n_draws finite joint scores. */
+int tco_idx_beam_step(const tco_params* p, const float* logits, size_t batch, size_t nb, size_t V,
+                      const uint32_t* hist_off, const uint32_t* hist_ids, const double* beam_scores,
+                      const double* uniforms, size_t n_draws, uint32_t* cand_flat, double* cand_scores,
+                      int32_t* status) {
+  if (p->variant != TCO_INDEXTTS) return TCO_EINVAL;
+  int st = check_params(p);
+  if (st != TCO_OK) return st;
+  float* x = (float*)malloc((V ? V : 1) * sizeof(float));
+  double* joint = (double*)malloc((nb * V > 0 ? nb * V : 1) * sizeof(double));
+  size_t* picks = (size_t*)malloc((n_draws ? n_draws : 1) * sizeof(size_t));
+  for (size_t bi = 0; bi < batch; bi++) {
+    for (size_t j = 0; j < nb; j++) {
+      const size_t r = bi * nb + j;
+      memcpy(x, logits + r * V, V * sizeof(float));
+      const uint32_t* ids = NULL;
+      size_t n_ids = 0;
+      if (hist_off && hist_ids) { ids = hist_ids + hist_off[r]; n_ids = hist_off[r + 1] - hist_off[r]; }
+      idx_process_row(p, x, V, ids, n_ids, NULL);
+      for (size_t i = 0; i < V; i++) joint[j * V + i] = (double)x[i] + beam_scores[r];
+    }
+    status[bi] = tco_idx_sample_wo_replacement(joint, nb * V, n_draws, uniforms + bi * n_draws, picks);
+    uint32_t* cf = cand_flat + bi * n_draws;
+    double* cs = cand_scores + bi * n_draws;
+    if (status[bi] != TCO_OK) {
+      for (size_t d = 0; d < n_draws; d++) { cf[d] = 0; cs[d] = 0.0; }
+      continue;
+    }
+    /* candidates.sort_by(|a, x| x.0.total_cmp(&a.0)): stable, descending */
+    for (size_t d = 0; d < n_draws; d++) {
+      size_t k = d;
+      const double v = joint[picks[d]];
+      while (k > 0 && tkey64(cs[k - 1]) < tkey64(v)) {
+        cs[k] = cs[k - 1];
+        cf[k] = cf[k - 1];
+        k--;
+      }
+      cs[k] = v;
+      cf[k] = (uint32_t)picks[d];
+    }
+  }
+  free(picks); free(joint); free(x);
+  return TCO_OK;
 }
 
 int tco_sample(const tco_params* p, const float* logits, size_t rows, size_t V,

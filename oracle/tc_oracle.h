@@ -127,6 +127,12 @@ void tco_idx_typical(float* row, size_t V, double mass, size_t min_keep); /* :20
 size_t tco_idx_inverse_cdf(const double* w, size_t n, double u);   /* :251-265 */
 int tco_idx_sample_wo_replacement(const double* scores, size_t n_scores, size_t n,
                                   const double* uniforms, size_t* out); /* :280-303 */
+/* one beam-sample step (:640-701): per element of nb beam rows, the joint
+ * scores, n_draws draws without replacement, candidates sorted descending */
+int tco_idx_beam_step(const tco_params* p, const float* logits, size_t batch, size_t nb, size_t V,
+                      const uint32_t* hist_off, const uint32_t* hist_ids, const double* beam_scores,
+                      const double* uniforms, size_t n_draws, uint32_t* cand_flat, double* cand_scores,
+                      int32_t* status);
 
 /* ---- cosyvoice3 (crates/cosyvoice3/src/llm.rs) ---- */
 uint32_t tco_cosy_nucleus(const float* probs, size_t V, float top_p, size_t top_k, float u0,

@@ -27,7 +27,7 @@ EXPORTS = (
     "tc_create", "tc_destroy", "tc_sample", "tc_apply_repetition_penalty",
     "tc_apply_repetition_penalty_with_mask", "tc_build_suppression_mask",
     "tc_apply_token_suppression_with_mask", "tc_update_penalty_mask", "tc_greedy_sample",
-    "tc_last_error", "tc_abi_version",
+    "tc_last_error", "tc_abi_version", "tc_indextts_beam_step",
 )
 
 
@@ -46,6 +46,7 @@ class SampleParams(C.Structure):
         ("exclude_id", C.c_int32),
         ("d_add_mask", C.c_void_p),
         ("d_pen_mask", C.c_void_p),
+        ("d_mark_mask", C.c_void_p),
     ]
 
 
@@ -101,6 +102,9 @@ def load(path: str = LIB_PATH):
     L.tc_update_penalty_mask.argtypes = [vp, sz, vp, vp]
     L.tc_greedy_sample.restype = C.c_int
     L.tc_greedy_sample.argtypes = [vp, C.c_int, sz, sz, sz, vp, vp]
+    L.tc_indextts_beam_step.restype = C.c_int
+    L.tc_indextts_beam_step.argtypes = [vp, C.POINTER(SampleParams), vp, C.c_int, sz, sz, sz, sz, vp, vp, vp, vp,
+                                        sz, vp, vp, vp, vp, vp]
     L.tc_last_error.restype = C.c_char_p
     L.tc_last_error.argtypes = []
     L.tc_abi_version.restype = C.c_int

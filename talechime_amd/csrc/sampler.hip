@@ -87,7 +87,20 @@ struct RowArgs {
   int ras_win;
   float ras_thresh;  // (f32)win * tau
   int fast;          // indextts, qwen: the streaming fast path applies (1 <= K <= 64 < V, sampling)
+  float* mark;       // optional [V] penalty mask: set to 1.0 at each row's sampled id
+  float* keep_scores;  // indextts beam step: the final score of each kept id, beside keep_ids
 };
+
+// Writes a row's result.  A row sampled cleanly also marks its token in the
+// penalty mask the next step reads (synthesis.rs:568-579 update_penalty_mask,
+// fused: ids >= V are ignored there too).  Called by one lane per row, after
+// every read of the row's inputs.
+__device__ __forceinline__ void put_result(const RowArgs& a, int row, uint32_t tok, int32_t st, uint32_t flags) {
+  a.out_ids[row] = tok;
+  if (a.out_status) a.out_status[row] = st;
+  if (a.out_flags) a.out_flags[row] = flags;
+  if (a.mark && st == 0 && tok < (uint32_t)a.V) a.mark[tok] = 1.0f;
+}
 
 struct SurvLds {
   uint64_t key[kSurvCap];
@@ -176,9 +189,7 @@ __device__ __forceinline__ void sort_survivors(SurvLds& sv, uint32_t n) {
 
 __device__ __forceinline__ void finish_row(const RowArgs& a, int row, uint32_t tok, int32_t st, uint32_t flags) {
   if (threadIdx.x == 0) {
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = st;
-    if (a.out_flags) a.out_flags[row] = flags;
+    put_result(a, row, tok, st, flags);
   }
 }
 
@@ -431,9 +442,7 @@ __device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, ui
     }
   }
   if (lane == 0) {
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = TC_OK;
-    if (a.out_flags) a.out_flags[row] = flags;
+    put_result(a, row, tok, TC_OK, flags);
     if (a.norm) a.norm[row] = S2;
     if (a.topk_count) a.topk_count[row] = ns;
     if (a.keep_count) a.keep_count[row] = (uint32_t)(__popcll(km0) + __popcll(km1));
@@ -632,9 +641,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
       uint64_t b = 0;
       for (int w = 0; w < num_waves(); ++w) b = wb[w] > b ? wb[w] : b;
       uint32_t tok = (b == 0 || s_out[0]) ? 0u : ~(uint32_t)(b & 0xffffffffu);
-      a.out_ids[row] = tok;
-      if (a.out_status) a.out_status[row] = TC_OK;
-      if (a.out_flags) a.out_flags[row] = TC_FLAG_GREEDY;
+      put_result(a, row, tok, TC_OK, TC_FLAG_GREEDY);
     }
     no_verify(a, row);
     return;
@@ -725,9 +732,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
         if (cum >= u) { tok = sv.idx[j]; break; }
       }
     }
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = TC_OK;
-    if (a.out_flags) a.out_flags[row] = flags;
+    put_result(a, row, tok, TC_OK, flags);
     s_out[2] = __float_as_uint(S2);
     if (a.norm) a.norm[row] = S2;
   }
@@ -940,9 +945,7 @@ __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
       }
       tok = sv.idx[pick != 0xffffffffu ? pick : last];
     }
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = st;
-    if (a.out_flags) a.out_flags[row] = 0u;
+    put_result(a, row, tok, st, 0u);
     s_out[0] = nl;
   }
   if (a.keep_count) {
@@ -954,6 +957,7 @@ __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
           if (c < a.cap) {
             a.keep_ids[(size_t)row * a.cap + c] = sv.idx[j];
             a.keep_probs[(size_t)row * a.cap + c] = (float)sv.w[j];
+            if (a.keep_scores) a.keep_scores[(size_t)row * a.cap + c] = sv.val[j];
           }
           ++c;
         }
@@ -1780,9 +1784,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_moss(RowArgs a) {
       draw -= sv.w[r];
       if (draw <= 0.0) { tok = sv.idx[(uint32_t)sv.key[r]]; break; }
     }
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = TC_OK;
-    if (a.out_flags) a.out_flags[row] = flags;
+    put_result(a, row, tok, TC_OK, flags);
     s_out[0] = keep;
     s.d[0] = sw;
   }
@@ -1924,9 +1926,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_nano(RowArgs a) {
       draw -= sv.w[j];
       if (sv.w[j] > 0.0 && draw <= 0.0) { tok = sv.idx[j]; st = TC_OK; break; }
     }
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = st;
-    if (a.out_flags) a.out_flags[row] = 0u;
+    put_result(a, row, tok, st, 0u);
     if (a.keep_count) {
       uint32_t c = 0;
       for (uint32_t j = 0; j < n; ++j)
@@ -2025,6 +2025,180 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_greedy(const InT* logits
   }
 }
 
+// ---------------------------------------------------------------- indextts beam-sample step
+// generation.rs:640-701 after the processors: per batch element, the kept
+// (finite) scores of its num_beams rows joined beam-major (flat index
+// beam * V + id) with each row's running beam score added in f64, then
+// sample_without_replacement with n_draws draws (280-303) and the candidates
+// sorted by score descending, stable (690).  The row pass (k_indextts with
+// keep_scores set) leaves each row's kept ids, ascending, and their scores.
+constexpr int kBeamCap = 1024;    // kept ids per beam row (the row pass stages at most kSurvCap)
+constexpr int kJointCap = 4096;   // kept entries per batch element
+constexpr int kBeamMaxDraws = 64;
+constexpr int kBeamMaxBeams = 64;
+
+struct BeamArgs {
+  int nb, V, n_draws;
+  const int32_t* row_status;
+  const uint32_t* row_flags;
+  const uint32_t* keep_count;
+  const uint32_t* keep_ids;   // [rows, kBeamCap]
+  const float* keep_scores;   // [rows, kBeamCap]
+  const double* beam_scores;  // [rows]
+  const double* uniforms;     // [batch, n_draws]
+  uint32_t* cand_flat;        // [batch, n_draws]
+  double* cand_scores;        // [batch, n_draws]
+  int32_t* out_status;        // [batch]
+  uint32_t* out_flags;        // [batch]
+};
+
+struct BeamLds {
+  double s[kJointCap];     // joint scores
+  double e[kJointCap];     // exp(s - max), then the normalised weights
+  uint32_t flat[kJointCap];
+  uint8_t gone[kJointCap];  // drawn already, or not finite
+  uint32_t off[kBeamMaxBeams + 1];
+  double ps[kBeamMaxDraws];
+  uint32_t pf[kBeamMaxDraws];
+  double bcast;
+  int32_t st;
+  uint32_t flags;
+};
+
+__device__ __forceinline__ uint64_t tkey64(double v) {  // f64::total_cmp as an unsigned key
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+__global__ void __launch_bounds__(64) k_beam_joint(BeamArgs b) {
+  __shared__ BeamLds B;
+  const int bi = blockIdx.x, lane = threadIdx.x, nb = b.nb, nd = b.n_draws;
+  if (lane == 0) {
+    int32_t st = TC_OK;
+    uint32_t flags = 0, o = 0;
+    for (int j = 0; j < nb; ++j) {
+      const int r = bi * nb + j;
+      const int32_t rs = b.row_status[r];
+      flags |= b.row_flags[r] & TC_FLAG_NEAR_TIE;
+      // a row without a finite score (TC_ETOOFEW) adds nothing to the joint row
+      const uint32_t c = rs == TC_OK ? b.keep_count[r] : 0u;
+      if (rs != TC_OK && rs != TC_ETOOFEW && st == TC_OK) st = rs;
+      if (c > (uint32_t)kBeamCap && st == TC_OK) st = TC_EUNSUPPORTED;
+      B.off[j] = o;
+      o += c <= (uint32_t)kBeamCap ? c : 0u;
+    }
+    B.off[nb] = o;
+    if (o > (uint32_t)kJointCap && st == TC_OK) st = TC_EUNSUPPORTED;
+    B.st = st;
+    B.flags = flags;
+  }
+  __syncthreads();
+  // every loop below stays inside the staged entries (L <= kJointCap when OK)
+  const uint32_t L = B.st == TC_OK ? B.off[nb] : 0u;
+  if (B.st == TC_OK) {
+    for (int j = 0; j < nb; ++j) {
+      const int r = bi * nb + j;
+      const uint32_t o = B.off[j], c = B.off[j + 1] - o;
+      const double bonus = b.beam_scores[r];
+      for (uint32_t k = (uint32_t)lane; k < c; k += 64u) {
+        const double js = (double)b.keep_scores[(size_t)r * kBeamCap + k] + bonus;
+        B.s[o + k] = js;
+        B.flat[o + k] = (uint32_t)j * (uint32_t)b.V + b.keep_ids[(size_t)r * kBeamCap + k];
+        B.gone[o + k] = __builtin_isfinite(js) ? 0 : 1;
+      }
+    }
+  }
+  __syncthreads();
+  uint32_t nlive = 0;
+  for (uint32_t k = (uint32_t)lane; k < L; k += 64u) nlive += B.gone[k] ? 0u : 1u;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) nlive += __shfl_xor(nlive, o);
+  const bool run = B.st == TC_OK && nlive >= (uint32_t)nd;
+  if (run) {
+    for (int d = 0; d < nd; ++d) {
+      double m = -__builtin_inf();
+      for (uint32_t k = (uint32_t)lane; k < L; k += 64u)
+        if (!B.gone[k]) m = rmaxd(m, B.s[k]);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) m = rmaxd(m, __shfl_xor(m, o));
+      for (uint32_t k = (uint32_t)lane; k < L; k += 64u)
+        if (!B.gone[k]) B.e[k] = tc_exp_d(B.s[k] - m);
+      __syncthreads();
+      if (lane == 0) {
+        double sum = -0.0;
+        for (uint32_t k = 0; k < L; ++k)
+          if (!B.gone[k]) sum += B.e[k];
+        B.bcast = sum;
+      }
+      __syncthreads();
+      const double sum = B.bcast;
+      for (uint32_t k = (uint32_t)lane; k < L; k += 64u)
+        if (!B.gone[k]) B.e[k] = B.e[k] / sum;
+      __syncthreads();
+      if (lane == 0) {
+        double total = -0.0;
+        for (uint32_t k = 0; k < L; ++k)
+          if (!B.gone[k]) total += B.e[k];
+        const double u = b.uniforms[(size_t)bi * nd + d] * total;
+        // inverse_cdf (251-265): the first positive weight whose running sum
+        // exceeds u, else the last positive one (index 0 of live when none is)
+        double acc = 0.0;
+        uint32_t last = 0xffffffffu, pick = 0xffffffffu;
+        bool near = false;
+        for (uint32_t k = 0; k < L; ++k) {
+          if (B.gone[k]) continue;
+          if (last == 0xffffffffu) last = k;
+          const double w = B.e[k];
+          if (w <= 0.0) continue;
+          last = k;
+          acc += w;
+          near = near || __builtin_fabs(acc - u) <= exp_margin() * total;
+          if (acc > u) {
+            pick = k;
+            break;
+          }
+        }
+        if (pick == 0xffffffffu) pick = last;
+        if (near) B.flags |= TC_FLAG_NEAR_TIE;
+        B.gone[pick] = 1;
+        B.ps[d] = B.s[pick];
+        B.pf[d] = B.flat[pick];
+      }
+      __syncthreads();
+    }
+  }
+  if (lane == 0) {
+    double* cs = b.cand_scores + (size_t)bi * nd;
+    uint32_t* cf = b.cand_flat + (size_t)bi * nd;
+    if (run) {
+      // candidates.sort_by(|a, x| x.0.total_cmp(&a.0)): stable, descending
+      for (int d = 1; d < nd; ++d) {
+        const double v = B.ps[d];
+        const uint32_t f = B.pf[d];
+        int k = d;
+        while (k > 0 && tkey64(B.ps[k - 1]) < tkey64(v)) {
+          B.ps[k] = B.ps[k - 1];
+          B.pf[k] = B.pf[k - 1];
+          --k;
+        }
+        B.ps[k] = v;
+        B.pf[k] = f;
+      }
+      for (int d = 0; d < nd; ++d) {
+        cs[d] = B.ps[d];
+        cf[d] = B.pf[d];
+      }
+    } else {
+      for (int d = 0; d < nd; ++d) {
+        cs[d] = 0.0;
+        cf[d] = 0u;
+      }
+    }
+    b.out_status[bi] = B.st != TC_OK ? B.st : (run ? TC_OK : TC_ETOOFEW);
+    if (b.out_flags) b.out_flags[bi] = B.flags;
+  }
+}
+
 }  // namespace tc
 
 // ====================================================================== C ABI
@@ -2033,6 +2207,7 @@ struct tc_ctx {
   size_t max_rows;
   size_t max_vocab;
   uint8_t* d_mask;  // [max_vocab] byte mask for tc_apply_repetition_penalty
+  void* d_beam;     // the beam step's row-pass workspace (first beam step), or NULL
 };
 
 namespace {
@@ -2127,7 +2302,7 @@ int tc_create(int device, size_t max_rows, size_t max_vocab, tc_ctx** out) {
   if (device < 0 || device >= n) return fail(TC_EINVAL, "tc_create: device %d of %d", device, n);
   if (max_vocab == 0 || max_vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_create: bad max_vocab");
   DeviceGuard g(device);
-  tc_ctx* c = new tc_ctx{device, max_rows, max_vocab, nullptr};
+  tc_ctx* c = new tc_ctx{device, max_rows, max_vocab, nullptr, nullptr};
   e = hipMalloc(&c->d_mask, max_vocab);
   if (e != hipSuccess) {
     delete c;
@@ -2141,13 +2316,16 @@ void tc_destroy(tc_ctx* ctx) {
   if (!ctx) return;
   DeviceGuard g(ctx->device);
   if (ctx->d_mask) (void)hipFree(ctx->d_mask);
+  if (ctx->d_beam) (void)hipFree(ctx->d_beam);
   delete ctx;
 }
 
-int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t rows,
-              size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
-              const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
-              const tc_verify_out* verify, tc_stream stream) {
+// tc_sample; keep_scores (indextts only, with verify outputs) also receives
+// the final score of each kept id.
+static int sample_impl(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t rows,
+                       size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+                       const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
+                       const tc_verify_out* verify, float* keep_scores, tc_stream stream) {
   if (!ctx || !p) return fail(TC_EINVAL, "tc_sample: ctx/params is NULL");
   if (rows == 0) return TC_OK;
   if (!d_logits || !d_out_ids || !d_uniforms) return fail(TC_EINVAL, "tc_sample: NULL device pointer");
@@ -2166,6 +2344,9 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
   a.hist_mode = p->hist_mode;
   a.pen_mask = p->d_pen_mask;
   a.add_mask = p->d_add_mask;
+  a.mark = p->d_mark_mask;
+  if (a.mark && rows > 1 && a.mark == p->d_pen_mask)
+    return fail(TC_EINVAL, "tc_sample: d_mark_mask equals d_pen_mask with %zu rows (the rows would race)", rows);
   a.uniforms = d_uniforms;
   a.out_ids = d_out_ids;
   a.out_status = d_out_status;
@@ -2181,6 +2362,7 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
     a.keep_ids = verify->d_keep_ids;
     a.keep_probs = verify->d_keep_probs;
     a.norm = verify->d_norm;
+    a.keep_scores = keep_scores;
   }
   a.eos_id = p->eos_id;
   a.exclude_id = p->exclude_id;
@@ -2283,6 +2465,123 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
   }
   if (e != hipSuccess) return hip_fail(e, "tc_sample launch");
   return TC_OK;
+}
+
+int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t rows,
+              size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+              const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
+              const tc_verify_out* verify, tc_stream stream) {
+  return sample_impl(ctx, p, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, d_uniforms, d_out_ids,
+                     d_out_status, d_out_flags, verify, nullptr, stream);
+}
+
+// The beam step's row-pass workspace, allocated on the context's first beam
+// step: per row kBeamCap kept ids, scores, probabilities and top-k ids, the
+// counts, statuses and flags, and a zero uniform per row (the row pass's own
+// draw is not used).
+struct BeamWs {
+  uint32_t* keep_ids;
+  float* keep_scores;
+  float* keep_probs;
+  uint32_t* topk_ids;
+  uint32_t* topk_count;
+  uint32_t* keep_count;
+  uint32_t* ids;
+  int32_t* status;
+  uint32_t* flags;
+  double* zero_u;
+};
+
+static BeamWs beam_ws(void* base, size_t R) {
+  const size_t C = (size_t)tc::kBeamCap;
+  char* p = static_cast<char*>(base);
+  BeamWs w;
+  w.zero_u = reinterpret_cast<double*>(p);
+  p += R * 8;
+  w.keep_ids = reinterpret_cast<uint32_t*>(p);
+  p += R * C * 4;
+  w.keep_scores = reinterpret_cast<float*>(p);
+  p += R * C * 4;
+  w.keep_probs = reinterpret_cast<float*>(p);
+  p += R * C * 4;
+  w.topk_ids = reinterpret_cast<uint32_t*>(p);
+  p += R * C * 4;
+  w.topk_count = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.keep_count = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.ids = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.status = reinterpret_cast<int32_t*>(p);
+  p += R * 4;
+  w.flags = reinterpret_cast<uint32_t*>(p);
+  return w;
+}
+
+static size_t beam_ws_bytes(size_t R) { return R * 8 + R * (size_t)tc::kBeamCap * 16 + R * 20; }
+
+int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
+                          size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
+                          const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
+                          size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
+                          uint32_t* d_out_flags, tc_stream stream) {
+  if (!ctx || !p) return fail(TC_EINVAL, "tc_indextts_beam_step: ctx/params is NULL");
+  if (p->variant != TC_INDEXTTS) return fail(TC_EINVAL, "tc_indextts_beam_step: variant must be TC_INDEXTTS");
+  if (batch == 0) return TC_OK;
+  if (!d_logits || !d_beam_scores || !d_uniforms || !d_cand_flat || !d_cand_scores || !d_out_status)
+    return fail(TC_EINVAL, "tc_indextts_beam_step: NULL device pointer");
+  if (num_beams == 0 || num_beams > (size_t)tc::kBeamMaxBeams)
+    return fail(TC_EINVAL, "tc_indextts_beam_step: num_beams %zu (1..%d)", num_beams, tc::kBeamMaxBeams);
+  if (n_draws == 0 || n_draws > (size_t)tc::kBeamMaxDraws)
+    return fail(TC_EINVAL, "tc_indextts_beam_step: n_draws %zu (1..%d)", n_draws, tc::kBeamMaxDraws);
+  if (vocab == 0 || vocab > (size_t)INT32_MAX || num_beams * vocab > (size_t)UINT32_MAX)
+    return fail(TC_EINVAL, "tc_indextts_beam_step: num_beams * vocab must fit 32 bits");
+  if (batch > (size_t)INT32_MAX / num_beams) return fail(TC_EINVAL, "tc_indextts_beam_step: batch too large");
+  const size_t rows = batch * num_beams;
+  if (rows > ctx->max_rows) return fail(TC_EINVAL, "tc_indextts_beam_step: %zu rows > context max %zu", rows, ctx->max_rows);
+  DeviceGuard g(ctx->device);
+  if (!ctx->d_beam) {
+    const size_t bytes = beam_ws_bytes(ctx->max_rows);
+    hipError_t e = hipMalloc(&ctx->d_beam, bytes);
+    if (e != hipSuccess) {
+      ctx->d_beam = nullptr;
+      return fail(TC_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    e = hipMemset(ctx->d_beam, 0, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset");
+  }
+  const BeamWs w = beam_ws(ctx->d_beam, ctx->max_rows);
+  tc_verify_out v{};
+  v.cap = (uint32_t)tc::kBeamCap;
+  v.d_topk_count = w.topk_count;
+  v.d_topk_ids = w.topk_ids;
+  v.d_keep_count = w.keep_count;
+  v.d_keep_ids = w.keep_ids;
+  v.d_keep_probs = w.keep_probs;
+  v.d_norm = nullptr;
+  tc_sample_params rp = *p;
+  rp.d_mark_mask = nullptr;
+  int rc = sample_impl(ctx, &rp, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, w.zero_u, w.ids,
+                       w.status, w.flags, &v, w.keep_scores, stream);
+  if (rc != TC_OK) return rc;
+  tc::BeamArgs b{};
+  b.nb = (int)num_beams;
+  b.V = (int)vocab;
+  b.n_draws = (int)n_draws;
+  b.row_status = w.status;
+  b.row_flags = w.flags;
+  b.keep_count = w.keep_count;
+  b.keep_ids = w.keep_ids;
+  b.keep_scores = w.keep_scores;
+  b.beam_scores = d_beam_scores;
+  b.uniforms = d_uniforms;
+  b.cand_flat = d_cand_flat;
+  b.cand_scores = d_cand_scores;
+  b.out_status = d_out_status;
+  b.out_flags = d_out_flags;
+  hipLaunchKernelGGL(tc::k_beam_joint, dim3((unsigned)batch), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), b);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TC_OK : hip_fail(e, "tc_indextts_beam_step launch");
 }
 
 static int grid_for(size_t n) {

@@ -668,9 +668,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
       if (ok && !close) {
         const uint32_t tok = rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u));
         if (lane == 0) {
-          a.out_ids[row] = tok;
-          if (a.out_status) a.out_status[row] = TC_OK;
-          if (a.out_flags) a.out_flags[row] = 0u;
+          put_result(a, row, tok, TC_OK, 0u);
         }
         return;
       }
@@ -766,14 +764,15 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
     // before it against the target
     const double mg = order_margin(nl) * sum2;
     const double a_pick = rl_f64(pick < 64 ? acc0 : acc1, (int)(pick & 63u));
-    bool close = __builtin_fabs(a_pick - target) <= mg;
+    // (a beam step draws later, over the joint kept sets: this draw is unused)
+    bool close = !a.keep_scores && __builtin_fabs(a_pick - target) <= mg;
     if (found) {
       const uint64_t below0 = pick < 64 ? (pz0 & ((1ull << pick) - 1ull)) : pz0;
       const uint64_t below1 = pick < 64 ? 0ull : (pz1 & ((1ull << (pick - 64u)) - 1ull));
       if (below1 || below0) {
         const uint32_t prev = below1 ? 64u + 63u - (uint32_t)__builtin_clzll(below1) : 63u - (uint32_t)__builtin_clzll(below0);
         const double a_prev = rl_f64(prev < 64 ? acc0 : acc1, (int)(prev & 63u));
-        close = close || __builtin_fabs(a_prev - target) <= mg;
+        close = close || (!a.keep_scores && __builtin_fabs(a_prev - target) <= mg);
       }
     }
     if (close) {
@@ -808,9 +807,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   }
   const uint32_t tok = nl ? rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u)) : 0u;
   if (lane == 0) {
-    a.out_ids[row] = tok;
-    if (a.out_status) a.out_status[row] = nl ? TC_OK : TC_ETOOFEW;
-    if (a.out_flags) a.out_flags[row] = flags;
+    put_result(a, row, tok, nl ? TC_OK : TC_ETOOFEW, flags);
     if (a.topk_count) {
       a.topk_count[row] = ns;
       a.keep_count[row] = nl;
@@ -831,6 +828,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
         if (j < a.cap) {
           a.keep_ids[(size_t)row * a.cap + j] = id[q];
           a.keep_probs[(size_t)row * a.cap + j] = (float)(e[q] / sum2);
+          if (a.keep_scores) a.keep_scores[(size_t)row * a.cap + j] = sc[q];
         }
       }
     }

@@ -15,14 +15,19 @@ from . import _lib
 from ._lib import (BF16, COSY_RAS, F32, HIST_MASK, HIST_PER_ROW, INDEXTTS, MOSS, MOSS_NANO, QWEN,
                    SampleParams, TcError, VerifyOut, check, load)
 
-__all__ = ["DeviceSampler", "make_params", "SampleResult", "QWEN", "COSY_RAS", "INDEXTTS", "MOSS",
+__all__ = ["DeviceSampler", "make_params", "SampleResult", "BeamCandidates", "QWEN", "COSY_RAS", "INDEXTTS", "MOSS",
            "MOSS_NANO", "TcError"]
 
 
 def make_params(variant: int, *, temperature: float = 1.0, top_p: float = 1.0, penalty: float = 1.0,
                 top_k: int = 0, min_keep: int = 2, ras_win: int = 10, ras_tau: float = 0.1,
                 eos_id: int = -1, exclude_id: int = -1, hist_mode: int = HIST_PER_ROW,
-                add_mask: torch.Tensor | None = None, pen_mask: torch.Tensor | None = None) -> SampleParams:
+                add_mask: torch.Tensor | None = None, pen_mask: torch.Tensor | None = None,
+                mark_mask: torch.Tensor | None = None) -> SampleParams:
+    """Parameters of one sampler step.  `mark_mask` ([V] f32 on the device)
+    receives 1.0 at each cleanly sampled row's id, the penalty-mask update of
+    synthesis.rs:568-579 fused into the step; it may be `pen_mask` itself for a
+    one-row step."""
     p = SampleParams()
     p.variant, p.hist_mode = variant, hist_mode
     p.temperature, p.top_p, p.repetition_penalty = float(temperature), float(top_p), float(penalty)
@@ -34,7 +39,10 @@ def make_params(variant: int, *, temperature: float = 1.0, top_p: float = 1.0, p
     if pen_mask is not None:
         _need_cuda(pen_mask, torch.float32, "pen_mask")
         p.d_pen_mask = pen_mask.data_ptr()
-    p._keep = (add_mask, pen_mask)  # keep the tensors alive with the struct
+    if mark_mask is not None:
+        _need_cuda(mark_mask, torch.float32, "mark_mask")
+        p.d_mark_mask = mark_mask.data_ptr()
+    p._keep = (add_mask, pen_mask, mark_mask)  # keep the tensors alive with the struct
     return p
 
 
@@ -103,6 +111,9 @@ class DeviceSampler:
         per_row = 2 if params.variant == COSY_RAS else 1
         if uniforms.numel() < rows * per_row:
             raise ValueError("not enough uniforms")
+        for m in params._keep:
+            if m is not None and m.numel() < V:
+                raise ValueError(f"masks need {V} entries, got {m.numel()}")
         ho = hi = None
         if hist_off is not None:
             _need_cuda(hist_off, None, "hist_off")
@@ -133,6 +144,58 @@ class DeviceSampler:
                               out.flags.data_ptr(), C.byref(ver) if ver is not None else None, st)
         check(rc)
         return out
+
+
+    def beam_step(self, params: SampleParams, logits: torch.Tensor, hist_off: torch.Tensor | None,
+                  hist_ids: torch.Tensor | None, beam_scores: torch.Tensor, num_beams: int,
+                  uniforms: torch.Tensor, n_draws: int | None = None, *,
+                  stream: torch.cuda.Stream | None = None) -> BeamCandidates:
+        """One indextts beam-sample step (generation.rs:640-701): the candidates
+        (flat index beam * V + id, joint score) of each batch element, by score
+        descending.  ``logits`` holds ``batch * num_beams`` rows, beam-major per
+        element; ``n_draws`` defaults to 2 * num_beams as in the reference."""
+        if params.variant != INDEXTTS:
+            raise ValueError("beam_step samples indextts rows")
+        if logits.dim() != 2 or logits.stride(1) != 1 or not logits.is_cuda:
+            raise ValueError("logits must be a 2-D GPU tensor with unit stride in the vocab dim")
+        dt = {torch.float32: F32, torch.bfloat16: BF16}.get(logits.dtype)
+        if dt is None:
+            raise ValueError(f"logits dtype {logits.dtype} (f32 or bf16 expected)")
+        rows, V = logits.shape
+        if num_beams < 1 or rows % num_beams:
+            raise ValueError("rows must be a multiple of num_beams")
+        batch = rows // num_beams
+        n_draws = 2 * num_beams if n_draws is None else n_draws
+        _need_cuda(beam_scores, torch.float64, "beam_scores")
+        _need_cuda(uniforms, torch.float64, "uniforms")
+        if beam_scores.numel() < rows or uniforms.numel() < batch * n_draws:
+            raise ValueError("beam_scores needs one score per row and uniforms n_draws per element")
+        ho = hi = None
+        if hist_off is not None:
+            _need_cuda(hist_off, None, "hist_off")
+            _need_cuda(hist_ids, None, "hist_ids")
+            if hist_off.element_size() != 4 or hist_ids.element_size() != 4 or hist_off.numel() < rows + 1:
+                raise ValueError("histories: rows + 1 32-bit offsets and 32-bit ids")
+            ho, hi = hist_off.data_ptr(), hist_ids.data_ptr() if hist_ids.numel() else hist_off.data_ptr()
+        dev = logits.device
+        out = BeamCandidates(torch.empty(batch, n_draws, dtype=torch.int32, device=dev),
+                             torch.empty(batch, n_draws, dtype=torch.float64, device=dev),
+                             torch.empty(batch, dtype=torch.int32, device=dev),
+                             torch.empty(batch, dtype=torch.int32, device=dev))
+        st = (stream or torch.cuda.current_stream(dev)).cuda_stream
+        check(load().tc_indextts_beam_step(self._ctx, C.byref(params), logits.data_ptr(), dt, batch, num_beams, V,
+                                           logits.stride(0), ho, hi, beam_scores.data_ptr(), uniforms.data_ptr(),
+                                           n_draws, out.flat.data_ptr(), out.scores.data_ptr(),
+                                           out.status.data_ptr(), out.flags.data_ptr(), st))
+        return out
+
+
+@dataclass
+class BeamCandidates:
+    flat: torch.Tensor    # [batch, n_draws] int32 (u32 bits): beam * V + id
+    scores: torch.Tensor  # [batch, n_draws] f64 joint scores, descending
+    status: torch.Tensor  # [batch] int32 tc_status
+    flags: torch.Tensor   # [batch] int32 tc_flag bits
 
 
 def launch_shape(vocab: int, dtype: int = F32) -> tuple[int, int]:

@@ -205,3 +205,33 @@ def make_batch(w: Workload, rows: int | None = None, batch_index: int = 0) -> Ba
     else:
         uniforms = _rng.unit_f64(seed, R * w.n_uniforms)
     return Batch(logits, logits_f32, hist_off, hist_ids, uniforms)
+
+
+@dataclass
+class BeamBatch:
+    logits: np.ndarray       # [batch * num_beams, V] f32; row bi * num_beams + j is beam j
+    hist_off: np.ndarray     # [rows + 1] u32
+    hist_ids: np.ndarray     # u32
+    beam_scores: np.ndarray  # [rows] f64 running beam scores
+    uniforms: np.ndarray     # [batch * n_draws] f64
+    num_beams: int
+    n_draws: int
+
+
+def make_beam_batch(w: Workload, batch: int, num_beams: int = 3, first_step: bool = False,
+                    batch_index: int = 0) -> BeamBatch:
+    """Inputs of one indextts beam-sample step over the seeded rows of ``w``:
+    ``batch`` elements of ``num_beams`` rows each, 2 * num_beams draws per
+    element (generation.rs:620).  The first step's beam scores are 0 for beam 0
+    and -1e9 for the others (generation.rs:582-585); later steps carry running
+    sums of log-probabilities."""
+    rows = batch * num_beams
+    b = make_batch(w, rows=rows, batch_index=batch_index)
+    seed = w.seed + 7777 * batch_index + 0xB3A
+    if first_step:
+        bonus = np.array([0.0 if r % num_beams == 0 else -1e9 for r in range(rows)])
+    else:
+        bonus = -_rng.unit_f64(seed, rows) * 40.0
+    n_draws = 2 * num_beams
+    return BeamBatch(b.logits_f32, b.hist_off, b.hist_ids, bonus, _rng.unit_f64(seed + 1, batch * n_draws),
+                     num_beams, n_draws)

@@ -142,7 +142,8 @@ def cosy_row(x, *, top_p, top_k, win, tau, hist, u0, u1, eos_id=-1):
 
 
 # ------------------------------------------------------------------ indextts
-def indextts_row(x, *, temperature, top_k, top_p, penalty, hist, u, min_keep=2):
+def indextts_scores(x, *, temperature, top_k, top_p, penalty, hist, min_keep=2):
+    """The processors of one row (generation.rs:643-662); f32 scores."""
     s = [F(v) for v in x]
     V = len(s)
     mx = F(-np.inf)
@@ -187,29 +188,60 @@ def indextts_row(x, *, temperature, top_k, top_p, penalty, hist, u, min_keep=2):
         for i in order[::-1][:min_keep]:
             remove.discard(i)
         s = [NEG if i in remove else v for i, v in enumerate(s)]
-    joint = [float(v) + 0.0 for v in s]
-    live = [i for i in range(V) if math.isfinite(joint[i])]
-    if not live:
+    return s
+
+
+def wo_replacement(joint, n, us):
+    """sample_without_replacement (generation.rs:280-303) over f64 scores with
+    the uniforms us[0..n); None when fewer than n are finite."""
+    live = [i for i in range(len(joint)) if math.isfinite(joint[i])]
+    if len(live) < n:
         return None
-    m = max(joint[i] for i in live)
-    ex = [math.exp(joint[i] - m) for i in live]
-    tot = -0.0
-    for v in ex:
-        tot += v
-    w = [v / tot for v in ex]
-    total = -0.0
-    for v in w:
-        total += v
-    uu = u * total
-    acc, last = 0.0, 0
-    for j, wv in enumerate(w):
-        if wv <= 0.0:
-            continue
-        last = j
-        acc += wv
-        if acc > uu:
-            return live[j]
-    return live[last]
+    out = []
+    for d in range(n):
+        m = max(joint[i] for i in live)
+        ex = [math.exp(joint[i] - m) for i in live]
+        tot = -0.0
+        for v in ex:
+            tot += v
+        w = [v / tot for v in ex]
+        total = -0.0
+        for v in w:
+            total += v
+        uu = us[d] * total
+        acc, last, pick = 0.0, 0, None
+        for j, wv in enumerate(w):
+            if wv <= 0.0:
+                continue
+            last = j
+            acc += wv
+            if acc > uu:
+                pick = j
+                break
+        pick = last if pick is None else pick
+        out.append(live.pop(pick))
+    return out
+
+
+def indextts_row(x, *, temperature, top_k, top_p, penalty, hist, u, min_keep=2):
+    s = indextts_scores(x, temperature=temperature, top_k=top_k, top_p=top_p, penalty=penalty, hist=hist,
+                        min_keep=min_keep)
+    r = wo_replacement([float(v) + 0.0 for v in s], 1, [u])
+    return None if r is None else r[0]
+
+
+def indextts_beam_step(rows, hists, bonus, num_beams, us, n_draws, **kw):
+    """generation.rs:640-701 for one batch element: the beam rows' scores
+    joined beam-major with each row's running score added, n_draws draws,
+    candidates (score, flat) sorted by score descending (a stable sort)."""
+    joint = []
+    for j in range(num_beams):
+        s = indextts_scores(rows[j], hist=hists[j], **kw)
+        joint += [float(v) + float(bonus[j]) for v in s]
+    picks = wo_replacement(joint, n_draws, us)
+    if picks is None:
+        return None
+    return sorted([(joint[f], f) for f in picks], key=lambda c: -c[0])
 
 
 # ------------------------------------------------------------------ moss

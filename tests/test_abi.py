@@ -29,12 +29,30 @@ def test_library_exports_every_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     lib.tc_abi_version.restype = ctypes.c_int
-    assert lib.tc_abi_version() == 1
+    assert lib.tc_abi_version() == 2
 
 
-def test_struct_layout_matches_header():
+def _c_layout(struct: str, fields):
+    """sizeof and offsetof of `struct` as gcc lays it out for the header."""
+    import subprocess
+    import tempfile
+    lines = [f'printf("%zu\\n", sizeof({struct}));']
+    lines += [f'printf("%zu\\n", offsetof({struct}, {f}));' for f in fields]
+    prog = ("#include <stdio.h>\n#include <stddef.h>\n#include \"talechime_hip.h\"\n"
+            "int main(void) {\n" + "\n".join(lines) + "\nreturn 0;\n}\n")
+    with tempfile.TemporaryDirectory() as d:
+        c, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
+        open(c, "w").write(prog)
+        subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout.split()
+    return int(out[0]), [int(x) for x in out[1:]]
+
+
+@pytest.mark.parametrize("cname,pyname", [("tc_sample_params", "SampleParams"), ("tc_verify_out", "VerifyOut")])
+def test_struct_layout_matches_header(cname, pyname):
     from talechime_amd import _lib
-    # offsets of tc_sample_params as laid out by the C compiler for this header
-    assert ctypes.sizeof(_lib.SampleParams) == 72
-    assert _lib.SampleParams.d_add_mask.offset == 56
-    assert ctypes.sizeof(_lib.VerifyOut) == 56
+    cls = getattr(_lib, pyname)
+    names = [f[0] for f in cls._fields_]
+    size, offs = _c_layout(cname, names)
+    assert ctypes.sizeof(cls) == size
+    assert [getattr(cls, n).offset for n in names] == offs

@@ -1,0 +1,135 @@
+"""Parity of the indextts beam-sample step (tc_indextts_beam_step, through the
+C ABI) with the oracle's restatement of generation.rs:640-701.
+
+Bar: candidate flat indices and joint scores bit-exact per batch element.
+Elements carrying TC_FLAG_NEAR_TIE (a top-p or draw decision within the f64
+exp error of the reference's libm) are counted, and only they may differ.
+"""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from talechime_amd import _lib, synth  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+W = synth.WORKLOADS["indextts-mel-256x8194"]
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    from talechime_amd.sampler import DeviceSampler
+    s = DeviceSampler(0, max_rows=1024, max_vocab=1 << 14)
+    yield s
+    s.close()
+
+
+def _kw(**over):
+    kw = dict(temperature=W.temperature, top_k=W.top_k, top_p=W.top_p, penalty=W.penalty, min_keep=2)
+    kw.update(over)
+    return kw
+
+
+def _run(sampler, logits, hist_off, hist_ids, bonus, nb, uniforms, n_draws, **kw):
+    from talechime_amd.sampler import make_params
+    x = np.ascontiguousarray(logits, np.float32)
+    dho = dhi = None
+    if hist_off is not None:
+        dho = torch.from_numpy(np.asarray(hist_off, np.uint32).view(np.int32).copy()).cuda()
+        ids = np.asarray(hist_ids, np.uint32)
+        dhi = torch.from_numpy((ids if ids.size else np.zeros(1, np.uint32)).view(np.int32).copy()).cuda()
+    p = make_params(_lib.INDEXTTS, penalty=kw.pop("penalty", 1.0), **kw)
+    r = sampler.beam_step(p, torch.from_numpy(x).cuda(), dho, dhi, torch.from_numpy(np.asarray(bonus, np.float64)).cuda(),
+                          nb, torch.from_numpy(np.asarray(uniforms, np.float64)).cuda(), n_draws)
+    torch.cuda.synchronize()
+    return {"flat": r.flat.cpu().numpy().view(np.uint32), "scores": r.scores.cpu().numpy(),
+            "status": r.status.cpu().numpy(), "flags": r.flags.cpu().numpy()}
+
+
+def _compare(g, o, name, **info):
+    near = (g["flags"] & 16) != 0
+    ok = ~near
+    assert np.array_equal(g["status"], o["status"]), (g["status"], o["status"])
+    good = ok & (o["status"] == 0)
+    diff = [bi for bi in np.nonzero(good)[0]
+            if not (np.array_equal(g["flat"][bi], o["flat"][bi])
+                    and np.array_equal(g["scores"][bi].view(np.int64), o["scores"][bi].view(np.int64)))]
+    print(f"[beam] {name} " + " ".join(f"{k}={v}" for k, v in info.items())
+          + f" elements={g['status'].size} near_tie={int(near.sum())} mismatch={len(diff)}", flush=True)
+    assert not diff, [(bi, g["flat"][bi], o["flat"][bi]) for bi in diff[:3]]
+
+
+@pytest.mark.parametrize("first_step", [True, False])
+@pytest.mark.parametrize("batch_index", [0, 1])
+def test_beam_step_workload(sampler, first_step, batch_index):
+    # 64 elements x 3 beams of the indextts mel-code rows (8194 f32 logits,
+    # history 1500, penalty 10, T 0.8, top-k 30, top-p 0.8), six draws each
+    bb = synth.make_beam_batch(W, 64, 3, first_step=first_step, batch_index=batch_index)
+    args = (bb.logits, bb.hist_off, bb.hist_ids, bb.beam_scores, 3, bb.uniforms, 6)
+    g = _run(sampler, *args, **_kw())
+    o = O.idx_beam_step(O.make_params(O.INDEXTTS, **_kw()), *args)
+    assert (o["status"] == 0).all()
+    _compare(g, o, "workload", first_step=first_step, batch=batch_index)
+    if first_step:
+        # the active beam's kept ids are drawn before the inactive beams refill
+        assert (g["flat"][:, :2] < W.vocab).all()
+
+
+@pytest.mark.parametrize("top_k,nb", [(200, 2), (0, 1), (5, 4)])
+def test_beam_step_shapes(sampler, top_k, nb):
+    # top-k 200: the general row path; top-k 0 with top-p 1: every finite score
+    # of a small vocabulary is live; 4 beams of top-k 5
+    g_ = np.random.default_rng(top_k + nb)
+    V = 8194 if top_k else 700
+    batch = 6
+    x = (g_.standard_normal((batch * nb, V)) * 4).astype(np.float32)
+    hist = g_.integers(0, V, (batch * nb, 40)).astype(np.uint32)
+    off = (np.arange(batch * nb + 1) * 40).astype(np.uint32)
+    bonus = -g_.random(batch * nb) * 10
+    n_draws = 2 * nb
+    u = g_.random(batch * n_draws)
+    kw = _kw(top_k=top_k, top_p=0.8 if top_k else 1.0)
+    g = _run(sampler, x, off, hist.reshape(-1), bonus, nb, u, n_draws, **kw)
+    o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, off, hist.reshape(-1), bonus, nb, u, n_draws)
+    _compare(g, o, "shapes", top_k=top_k, nb=nb)
+
+
+def test_beam_step_too_few_and_nan_rows(sampler):
+    g_ = np.random.default_rng(9)
+    V, nb = 300, 3
+    x = (g_.standard_normal((4 * nb, V)) * 3).astype(np.float32)
+    x[1, 7] = np.nan  # beam 1 of element 0: every score NaN, nothing live in it
+    kw = _kw(top_k=2, top_p=0.1, penalty=1.0)
+    bonus = np.zeros(4 * nb)
+    # two kept ids per live row: element 0 has 4 finite joint scores, the others 6
+    for n_draws, want_ok in ((4, [1, 1, 1, 1]), (6, [0, 1, 1, 1]), (7, [0, 0, 0, 0])):
+        u = g_.random(4 * n_draws)
+        g = _run(sampler, x, None, None, bonus, nb, u, n_draws, **kw)
+        o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, None, None, bonus, nb, u, n_draws)
+        assert list(o["status"] == 0) == [bool(v) for v in want_ok]
+        _compare(g, o, "too-few", n_draws=n_draws)
+
+
+def test_beam_step_rejects_bad_arguments(sampler):
+    from talechime_amd.sampler import make_params
+    x = torch.zeros(6, 100, device="cuda")
+    b = torch.zeros(6, dtype=torch.float64, device="cuda")
+    u = torch.zeros(12, dtype=torch.float64, device="cuda")
+    with pytest.raises(ValueError):
+        sampler.beam_step(make_params(_lib.QWEN), x, None, None, b, 3, u)
+    p = make_params(_lib.INDEXTTS, top_k=5)
+    with pytest.raises(_lib.TcError):  # more than 64 draws
+        sampler.beam_step(p, x, None, None, b, 3, torch.zeros(2 * 65, dtype=torch.float64, device="cuda"), 65)
+    L = _lib.load()
+    cf = torch.zeros(12, dtype=torch.int32, device="cuda")
+    cs = torch.zeros(12, dtype=torch.float64, device="cuda")
+    st = torch.zeros(2, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    import ctypes
+    rc = L.tc_indextts_beam_step(sampler.ctx, ctypes.byref(p), x.data_ptr(), 0, 2, 0, 100, 100, None, None,
+                                 b.data_ptr(), u.data_ptr(), 6, cf.data_ptr(), cs.data_ptr(), st.data_ptr(), None, s)
+    assert rc == _lib.TC_EINVAL  # num_beams 0

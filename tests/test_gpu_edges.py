@@ -255,6 +255,77 @@ def test_qwen_penalty_modes_and_masks(sampler):
     same(g, o)
 
 
+def _talker_loop(sampler, top_k, steps=24, min_new=6):
+    """The qwen talker's per-step chain (synthesis.rs:546-579, 1228-1279) with the
+    penalty-mask update fused into the step: one row, the mask read and marked in
+    the same launch, suppression and min-new-token EOS on."""
+    g_ = np.random.default_rng(31 + top_k)
+    V, eos = 3072, 2150
+    sup = O.qwen_suppression_mask(V, eos)
+    dsup = torch.from_numpy(sup).cuda()
+    host_mask = np.zeros(V, np.float32)
+    dmask = torch.zeros(V, dtype=torch.float32, device="cuda")
+    rng = O.QwenRng(42)
+    dho = torch.zeros(2, dtype=torch.int32, device="cuda")
+    dhi = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got, want = [], []
+    hot = g_.integers(0, 2048, 4)
+    for step in range(steps):
+        x = (g_.standard_normal((1, V)) * 2.5).astype(np.float32)
+        x[0, hot] += 6.0  # the same few likely tokens each step, so tokens repeat
+        u = np.array([rng.rand_f32()], np.float32)
+        eos_id = eos if step < min_new else -1
+        kw = dict(temperature=0.9, top_k=top_k, top_p=0.8, penalty=1.05, eos_id=eos_id)
+        p = make_params(O.QWEN, hist_mode=2, add_mask=dsup, pen_mask=dmask, mark_mask=dmask, **kw)
+        r = sampler.sample(p, torch.from_numpy(x).cuda(), dho, dhi, torch.from_numpy(u).cuda())
+        torch.cuda.synchronize()
+        assert r.status.cpu().item() == 0
+        got.append(int(r.ids.cpu().numpy().view(np.uint32)[0]))
+        op = O.make_params(O.QWEN, hist_mode=2, add_mask=sup, pen_mask=host_mask.copy(), **kw)
+        o = O.sample(op, x, np.zeros(2, np.uint32), np.zeros(0, np.uint32), u, cap=CAP)
+        want.append(int(o["ids"][0]))
+        if want[-1] < V:
+            host_mask[want[-1]] = 1.0  # synthesis.rs:572-577
+    return got, want, dmask.cpu().numpy(), host_mask
+
+
+@pytest.mark.parametrize("top_k", [50, 200])
+def test_qwen_talker_loop_with_fused_mask_update(sampler, top_k):
+    # top_k 50 runs the streaming fast path, 200 the general one
+    got, want, dmask, host_mask = _talker_loop(sampler, top_k)
+    assert got == want
+    assert np.array_equal(dmask, host_mask)
+    assert len(set(got)) < len(got)  # tokens repeat: the penalty met ids already marked
+
+
+def test_mark_mask_rows_and_aliasing(sampler):
+    g_ = np.random.default_rng(41)
+    V, rows = 3072, 16
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    u = torch.from_numpy(g_.random(rows).astype(np.float32)).cuda()
+    dx = torch.from_numpy(x).cuda()
+    dho = torch.zeros(rows + 1, dtype=torch.int32, device="cuda")
+    dhi = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pm = torch.zeros(V, dtype=torch.float32, device="cuda")
+    pm[g_.integers(0, V, 50)] = 1.0
+    mark = pm.clone()
+    p = make_params(O.QWEN, hist_mode=2, pen_mask=pm, mark_mask=mark, temperature=0.9, top_k=50,
+                    top_p=0.9, penalty=1.3)
+    r = sampler.sample(p, dx, dho, dhi, u)
+    q = make_params(O.QWEN, hist_mode=2, pen_mask=pm, temperature=0.9, top_k=50, top_p=0.9, penalty=1.3)
+    r0 = sampler.sample(q, dx, dho, dhi, u)
+    torch.cuda.synchronize()
+    ids = r.ids.cpu().numpy().view(np.uint32)
+    assert np.array_equal(ids, r0.ids.cpu().numpy().view(np.uint32))
+    want = pm.cpu().numpy()
+    want[ids] = 1.0
+    assert np.array_equal(mark.cpu().numpy(), want)
+    # a mask marked while other rows still read it would race: refused
+    bad = make_params(O.QWEN, hist_mode=2, pen_mask=pm, mark_mask=pm, temperature=0.9, top_k=50, penalty=1.3)
+    with pytest.raises(_lib.TcError):
+        sampler.sample(bad, dx, dho, dhi, u)
+
+
 # ------------------------------------------------------------------ indextts
 def test_indextts_random_rows(sampler):
     g_ = np.random.default_rng(11)

@@ -113,3 +113,53 @@ def test_small_random_rows_all_variants(oracle, seed):
                       x, off, hist, u2)
     want, ras = np_ref.cosy_row(x[0], top_p=tp, top_k=k, win=5, tau=0.2, hist=hist, u0=u2[0], u1=u2[1])
     assert r["ids"][0] == want and bool(r["flags"][0] & oracle.FLAG_RAS) == ras
+
+
+# ------------------------------------------------------------------ indextts beam-sample step
+def _beam_kw(w):
+    return dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty, min_keep=2)
+
+
+@pytest.mark.parametrize("first_step", [True, False])
+def test_indextts_beam_step(oracle, first_step):
+    # generation.rs:640-701: joint beam-major scores plus the beam score, six
+    # draws without replacement, candidates by score descending
+    w = synth.WORKLOADS["indextts-mel-256x8194"]
+    bb = synth.make_beam_batch(w, 2, 3, first_step=first_step)
+    p = oracle.make_params(oracle.INDEXTTS, **_beam_kw(w))
+    r = oracle.idx_beam_step(p, bb.logits, bb.hist_off, bb.hist_ids, bb.beam_scores, 3, bb.uniforms, 6)
+    for bi in range(2):
+        rows = [bb.logits[bi * 3 + j] for j in range(3)]
+        hists = [bb.hist_ids[bb.hist_off[bi * 3 + j]:bb.hist_off[bi * 3 + j + 1]] for j in range(3)]
+        want = np_ref.indextts_beam_step(rows, hists, bb.beam_scores[bi * 3:bi * 3 + 3], 3,
+                                         bb.uniforms[bi * 6:bi * 6 + 6], 6, **_beam_kw(w))
+        assert r["status"][bi] == oracle.OK
+        assert [(float(s), int(f)) for s, f in zip(r["scores"][bi], r["flat"][bi])] == want
+        if first_step:
+            # the active beam's kept set is drawn first; inactive beams refill the rest
+            # (generation.rs:266-271)
+            assert all(f < w.vocab for f in r["flat"][bi][:2])
+
+
+def test_indextts_beam_step_one_beam_is_the_row_sampler(oracle):
+    # one beam, one draw, beam score 0: the per-row sampler's id
+    w = synth.WORKLOADS["indextts-mel-256x8194"]
+    b = _rows(w, 6)
+    p = oracle.make_params(oracle.INDEXTTS, **_beam_kw(w))
+    r = oracle.sample(p, b.logits_f32, b.hist_off, b.hist_ids, b.uniforms)
+    rb = oracle.idx_beam_step(p, b.logits_f32, b.hist_off, b.hist_ids, np.zeros(6), 1, b.uniforms, 1)
+    assert np.array_equal(rb["flat"][:, 0], r["ids"])
+
+
+def test_indextts_beam_step_too_few(oracle):
+    # generation.rs:284-286: fewer finite joint scores than draws
+    g = np.random.default_rng(3)
+    x = (g.standard_normal((2, 50)) * 4).astype(np.float32)
+    p = oracle.make_params(oracle.INDEXTTS, temperature=1.0, top_k=2, top_p=0.1, min_keep=2)
+    r = oracle.idx_beam_step(p, x, None, None, np.zeros(2), 1, g.random(12), 6)
+    assert list(r["status"]) == [oracle.ETOOFEW] * 2
+    # two beams of two kept ids each, four draws: every kept id once
+    r = oracle.idx_beam_step(p, x, None, None, np.zeros(2), 2, g.random(4), 4)
+    k = oracle.sample(p, x, None, None, g.random(2), cap=8)
+    want = sorted([j * 50 + int(i) for j in range(2) for i in k["keep_ids"][j][:k["keep_count"][j]]])
+    assert r["status"][0] == oracle.OK and sorted(r["flat"][0].tolist()) == want
