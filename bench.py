@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--pool-mb", type=int, default=640, help="rotating input pool (MB of logits)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--beam", type=int, default=0, metavar="B",
+                    help="time the indextts beam-sample step over B elements x 3 beams instead")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the timed region, copy 256 MiB three times (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
@@ -80,6 +82,74 @@ def cpu_baseline(w, batch, seconds: float):
                       f"single thread, {dt:.1f} s"}
 
 
+def beam_bench(args):
+    """The indextts beam-sample step (tc_indextts_beam_step) over B elements of
+    3 beams of the mel-code rows, 6 draws each, timed like the sampler step:
+    a HIP graph of launches over a rotating pool, replayed."""
+    import torch
+
+    from talechime_amd import synth
+    from talechime_amd.sampler import DeviceSampler, make_params
+
+    w = synth.WORKLOADS["indextts-mel-256x8194"]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    nb, B = 3, args.beam
+    bb = synth.make_beam_batch(w, B, nb)
+    rows = B * nb
+    per_batch = rows * w.vocab * 4
+    n_pool = min(256, max(2, int(np.ceil(args.pool_mb * 1e6 / per_batch))))
+    g = torch.Generator(device=dev)
+    g.manual_seed(w.seed)
+    first = torch.from_numpy(bb.logits).to(dev)
+    logits = [first] + [torch.randn(first.shape, generator=g, device=dev) * w.sigma for _ in range(n_pool - 1)]
+    hoff = torch.from_numpy(bb.hist_off.view(np.int32).copy()).to(dev)
+    hid = torch.from_numpy(bb.hist_ids.view(np.int32).copy()).to(dev)
+    bs = torch.from_numpy(bb.beam_scores).to(dev)
+    un = torch.from_numpy(bb.uniforms).to(dev)
+    sampler = DeviceSampler(0, max_rows=rows, max_vocab=w.vocab)
+    p = make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
+                    min_keep=w.min_keep)
+    outs = [None] * n_pool
+
+    def step(j):
+        outs[j] = sampler.beam_step(p, logits[j], hoff, hid, bs, nb, un)
+
+    for i in range(max(args.warmup, n_pool)):
+        step(i % n_pool)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for j in range(n_pool):
+            step(j)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, -(-args.steps // n_pool))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    steps = replays * n_pool
+    ms = e0.elapsed_time(e1) / steps
+    st = outs[0].status.cpu().numpy()
+    if (st != 0).any():
+        print(f"bench.py: {int((st != 0).sum())} beam elements returned a non-OK status", file=sys.stderr)
+        sys.exit(1)
+    sampler.close()
+    print(json.dumps({
+        "metric": f"indextts beam-sample steps/sec ({B} elements x {nb} beams x {w.vocab}, 6 draws)",
+        "value": round(1e3 / ms, 1), "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded mel-code rows, running beam scores; rotating pool)",
+        "config": {"workload": f"indextts-beam-{B}x{nb}x{w.vocab}", "elements": B, "num_beams": nb,
+                   "n_draws": 2 * nb, "pool_batches": n_pool},
+        "timing": f"{replays} replays of a HIP graph of {n_pool} steps (row pass + joint draws each)",
+    }), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -87,6 +157,8 @@ def main():
               "(rows are independent: each GPU would run the same kernel on its share of the batch)",
               file=sys.stderr)
         sys.exit(2)
+    if args.beam:
+        return beam_bench(args)
     import torch
 
     from talechime_amd import synth

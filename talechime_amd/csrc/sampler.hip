@@ -2061,7 +2061,6 @@ struct BeamLds {
   double ps[kBeamMaxDraws];
   uint32_t pf[kBeamMaxDraws];
   double bcast;
-  int32_t st;
   uint32_t flags;
 };
 
@@ -2070,51 +2069,227 @@ __device__ __forceinline__ uint64_t tkey64(double v) {  // f64::total_cmp as an 
   return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
 }
 
+// The n_draws draws of one element with its L <= 64 * NS joint entries in
+// registers (entry k at slot k / 64 of lane k % 64).  A draw compares the
+// prefix scan of e = exp(s - max) (tree order) against u * (its total): in
+// exact arithmetic the reference's acc > u * total over w = e / sum.
+// order_margin bounds what separates the two (the sequential sums, the
+// divisions, exp's difference from libm); a draw whose decision falls inside
+// it runs the reference's sequential loops.  e is recomputed only when the
+// maximum changes: exp(s - max) of an unchanged maximum is the same value.
+// Call with every lane active.
+template <int NS>
+__device__ __forceinline__ bool beam_draws_reg(const BeamArgs& b, BeamLds& B, uint32_t L, int bi, uint32_t off,
+                                               double bonus, double ud, uint32_t* flags_io) {
+  const int lane = lane_id(), nd = b.n_draws, nb = b.nb;
+  double s[NS], e[NS];
+  uint32_t f[NS];
+  bool live[NS];
+  uint32_t nlive = 0;
+#pragma unroll
+  for (int q = 0; q < NS; ++q) {
+    // entry k belongs to the last beam whose offset is <= k (beams without
+    // kept ids share their offset with the next one)
+    const uint32_t k = (uint32_t)(q * kWave + lane);
+    uint32_t jj = 0, oj = 0;
+    double bj = 0.0;
+    for (int j = 0; j < nb; ++j) {
+      const uint32_t o = rl_u32(off, j);
+      const double bo = rl_f64(bonus, j);
+      if (k >= o) {
+        jj = (uint32_t)j;
+        oj = o;
+        bj = bo;
+      }
+    }
+    s[q] = 0.0;
+    f[q] = 0u;
+    if (k < L) {
+      const size_t at = (size_t)(bi * nb + (int)jj) * kBeamCap + (k - oj);
+      s[q] = (double)b.keep_scores[at] + bj;
+      f[q] = jj * (uint32_t)b.V + b.keep_ids[at];
+    }
+    live[q] = k < L && __builtin_isfinite(s[q]);
+    e[q] = 0.0;
+    nlive += (uint32_t)__popcll(__ballot(live[q]));
+  }
+  if (nlive < (uint32_t)nd) return false;
+  const double mg_rel = order_margin(L);
+  double m_prev = __builtin_nan("");
+  uint32_t flags = 0;
+  for (int d = 0; d < nd; ++d) {
+    double m = -__builtin_inf();
+#pragma unroll
+    for (int q = 0; q < NS; ++q) m = live[q] ? rmaxd(m, s[q]) : m;
+    m = dpp_wave_max_d(m);
+    if (!(m == m_prev)) {
+#pragma unroll
+      for (int q = 0; q < NS; ++q) e[q] = live[q] ? tc_exp_d(s[q] - m) : 0.0;
+      m_prev = m;
+    }
+    bool tiny = false;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) tiny = tiny || (e[q] > 0.0 && e[q] < 0x1p-1000);  // e / sum may round to 0
+    double carry = 0.0, c[NS];
+    uint64_t pos[NS], hit[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      c[q] = dpp_scan_f64(e[q]) + carry;
+      carry = rl_f64(c[q], kWave - 1);
+    }
+    const double u = rl_f64(ud, d);
+    const double total = carry, target = u * total;
+    uint32_t pick = 0xffffffffu, lastp = 0xffffffffu;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      pos[q] = __ballot(e[q] > 0.0);  // removed entries hold e = 0
+      hit[q] = __ballot(e[q] > 0.0 && c[q] > target);
+      if (pick == 0xffffffffu && hit[q]) pick = (uint32_t)(q * kWave + __builtin_ctzll(hit[q]));
+      if (pos[q]) lastp = (uint32_t)(q * kWave + 63 - __builtin_clzll(pos[q]));
+    }
+    const bool found = pick != 0xffffffffu;
+    if (!found) pick = lastp;
+    // the running sums at the pick and at the positive entry before it
+    uint32_t prev = 0xffffffffu;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      const int qp = (int)(pick >> 6);
+      uint64_t below = 0ull;
+      if (q < qp) below = pos[q];
+      else if (q == qp) below = pos[q] & ((1ull << (pick & 63u)) - 1ull);
+      if (below) prev = (uint32_t)(q * kWave + 63 - __builtin_clzll(below));
+    }
+    double a_pick = 0.0, a_prev = 0.0;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      if (pick != 0xffffffffu && (int)(pick >> 6) == q) a_pick = rl_f64(c[q], (int)(pick & 63u));
+      if (prev != 0xffffffffu && (int)(prev >> 6) == q) a_prev = rl_f64(c[q], (int)(prev & 63u));
+    }
+    const double mg = mg_rel * total;
+    bool close = __ballot(tiny) != 0ull || lastp == 0xffffffffu || __builtin_fabs(a_pick - target) <= mg;
+    if (found && prev != 0xffffffffu) close = close || __builtin_fabs(a_prev - target) <= mg;
+    if (close) {
+      // the reference's order: sequential sums over live entries in flat order
+      uint64_t lm[NS];
+#pragma unroll
+      for (int q = 0; q < NS; ++q) lm[q] = __ballot(live[q]);
+      double S = -0.0;
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        for (uint64_t mm = lm[q]; mm; mm &= mm - 1) S += rl_f64(e[q], __builtin_ctzll(mm));
+      double wv[NS];
+#pragma unroll
+      for (int q = 0; q < NS; ++q) wv[q] = live[q] ? e[q] / S : 0.0;
+      double tot = -0.0;
+#pragma unroll
+      for (int q = 0; q < NS; ++q)
+        for (uint64_t mm = lm[q]; mm; mm &= mm - 1) tot += rl_f64(wv[q], __builtin_ctzll(mm));
+      const double ue = u * tot;
+      double acc = 0.0;
+      uint32_t last = 0xffffffffu, pk = 0xffffffffu;
+      bool near = false;
+#pragma unroll
+      for (int q = 0; q < NS; ++q) {
+        for (uint64_t mm = lm[q]; mm && pk == 0xffffffffu; mm &= mm - 1) {
+          const uint32_t k = (uint32_t)(q * kWave + __builtin_ctzll(mm));
+          if (last == 0xffffffffu) last = k;  // last_positive starts at live[0]
+          const double wc = rl_f64(wv[q], __builtin_ctzll(mm));
+          if (wc <= 0.0) continue;
+          last = k;
+          acc += wc;
+          near = near || __builtin_fabs(acc - ue) <= exp_margin() * tot;
+          if (acc > ue) pk = k;
+        }
+      }
+      pick = pk != 0xffffffffu ? pk : last;
+      if (near) flags |= TC_FLAG_NEAR_TIE;
+    }
+    double ps = 0.0;
+    uint32_t pf = 0u;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) {
+      if ((int)(pick >> 6) == q) {
+        ps = rl_f64(s[q], (int)(pick & 63u));
+        pf = rl_u32(f[q], (int)(pick & 63u));
+        if (lane == (int)(pick & 63u)) {
+          live[q] = false;
+          e[q] = 0.0;
+        }
+      }
+    }
+    if (lane == 0) {
+      B.ps[d] = ps;
+      B.pf[d] = pf;
+    }
+  }
+  *flags_io |= flags;
+  return true;
+}
+
 __global__ void __launch_bounds__(64) k_beam_joint(BeamArgs b) {
   __shared__ BeamLds B;
   const int bi = blockIdx.x, lane = threadIdx.x, nb = b.nb, nd = b.n_draws;
-  if (lane == 0) {
-    int32_t st = TC_OK;
-    uint32_t flags = 0, o = 0;
-    for (int j = 0; j < nb; ++j) {
-      const int r = bi * nb + j;
-      const int32_t rs = b.row_status[r];
-      flags |= b.row_flags[r] & TC_FLAG_NEAR_TIE;
-      // a row without a finite score (TC_ETOOFEW) adds nothing to the joint row
-      const uint32_t c = rs == TC_OK ? b.keep_count[r] : 0u;
-      if (rs != TC_OK && rs != TC_ETOOFEW && st == TC_OK) st = rs;
-      if (c > (uint32_t)kBeamCap && st == TC_OK) st = TC_EUNSUPPORTED;
-      B.off[j] = o;
-      o += c <= (uint32_t)kBeamCap ? c : 0u;
-    }
-    B.off[nb] = o;
-    if (o > (uint32_t)kJointCap && st == TC_OK) st = TC_EUNSUPPORTED;
-    B.st = st;
-    B.flags = flags;
+  // one round of loads: the beam rows (lane j) and the element's uniforms (lane d)
+  int32_t rs = TC_OK;
+  uint32_t rf = 0u, cnt = 0u;
+  double bonus = 0.0, ud = 0.0;
+  if (lane < nb) {
+    const int r = bi * nb + lane;
+    rs = b.row_status[r];
+    rf = b.row_flags[r] & TC_FLAG_NEAR_TIE;
+    cnt = b.keep_count[r];
+    bonus = b.beam_scores[r];
   }
-  __syncthreads();
-  // every loop below stays inside the staged entries (L <= kJointCap when OK)
-  const uint32_t L = B.st == TC_OK ? B.off[nb] : 0u;
-  if (B.st == TC_OK) {
+  if (lane < nd) ud = b.uniforms[(size_t)bi * nd + lane];
+  // a row without a finite score (TC_ETOOFEW) adds nothing to the joint row;
+  // the first other failing row gives the element its status
+  const uint64_t fm = __ballot(lane < nb && rs != TC_OK && rs != TC_ETOOFEW);
+  int32_t st = fm ? (int32_t)rl_u32((uint32_t)rs, __builtin_ctzll(fm)) : TC_OK;
+  uint32_t c = (lane < nb && rs == TC_OK) ? cnt : 0u;
+  if (__ballot(c > (uint32_t)kBeamCap) && st == TC_OK) st = TC_EUNSUPPORTED;
+  c = c > (uint32_t)kBeamCap ? 0u : c;
+  const uint32_t incl = dpp_scan_u32(c);
+  const uint32_t off = incl - c;
+  const uint32_t Lall = rl_u32(incl, kWave - 1);
+  if (Lall > (uint32_t)kJointCap && st == TC_OK) st = TC_EUNSUPPORTED;
+  uint32_t flags = dpp_wave_or(rf);
+  // every loop below stays inside the element's entries (L <= kJointCap when OK)
+  const uint32_t L = st == TC_OK ? Lall : 0u;
+  bool run = false;
+  if (st == TC_OK && L <= 64u) {
+    run = beam_draws_reg<1>(b, B, L, bi, off, bonus, ud, &flags);
+  } else if (st == TC_OK && L <= 128u) {
+    run = beam_draws_reg<2>(b, B, L, bi, off, bonus, ud, &flags);
+  } else if (st == TC_OK && L <= 256u) {
+    run = beam_draws_reg<4>(b, B, L, bi, off, bonus, ud, &flags);
+  } else if (st == TC_OK) {
+    // more entries than registers hold: staged in LDS, the reference's loops on one lane
+    if (lane < nb) B.off[lane] = off;
+    if (lane == 0) {
+      B.off[nb] = L;
+      B.flags = flags;
+    }
+    __syncthreads();
     for (int j = 0; j < nb; ++j) {
       const int r = bi * nb + j;
-      const uint32_t o = B.off[j], c = B.off[j + 1] - o;
-      const double bonus = b.beam_scores[r];
-      for (uint32_t k = (uint32_t)lane; k < c; k += 64u) {
-        const double js = (double)b.keep_scores[(size_t)r * kBeamCap + k] + bonus;
+      const uint32_t o = B.off[j], cj = B.off[j + 1] - o;
+      const double bo = rl_f64(bonus, j);
+      for (uint32_t k = (uint32_t)lane; k < cj; k += 64u) {
+        const double js = (double)b.keep_scores[(size_t)r * kBeamCap + k] + bo;
         B.s[o + k] = js;
         B.flat[o + k] = (uint32_t)j * (uint32_t)b.V + b.keep_ids[(size_t)r * kBeamCap + k];
         B.gone[o + k] = __builtin_isfinite(js) ? 0 : 1;
       }
     }
-  }
-  __syncthreads();
-  uint32_t nlive = 0;
-  for (uint32_t k = (uint32_t)lane; k < L; k += 64u) nlive += B.gone[k] ? 0u : 1u;
+    __syncthreads();
+    uint32_t nlive = 0;
+    for (uint32_t k = (uint32_t)lane; k < L; k += 64u) nlive += B.gone[k] ? 0u : 1u;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) nlive += __shfl_xor(nlive, o);
-  const bool run = B.st == TC_OK && nlive >= (uint32_t)nd;
-  if (run) {
+    for (int o = 32; o > 0; o >>= 1) nlive += __shfl_xor(nlive, o);
+    run = nlive >= (uint32_t)nd;
+  }
+  if (run && L > 256u) {
+    // more entries than registers hold: the reference's loops on one lane
     for (int d = 0; d < nd; ++d) {
       double m = -__builtin_inf();
       for (uint32_t k = (uint32_t)lane; k < L; k += 64u)
@@ -2166,6 +2341,7 @@ __global__ void __launch_bounds__(64) k_beam_joint(BeamArgs b) {
       }
       __syncthreads();
     }
+    flags = B.flags;
   }
   if (lane == 0) {
     double* cs = b.cand_scores + (size_t)bi * nd;
@@ -2194,8 +2370,8 @@ __global__ void __launch_bounds__(64) k_beam_joint(BeamArgs b) {
         cf[d] = 0u;
       }
     }
-    b.out_status[bi] = B.st != TC_OK ? B.st : (run ? TC_OK : TC_ETOOFEW);
-    if (b.out_flags) b.out_flags[bi] = B.flags;
+    b.out_status[bi] = st != TC_OK ? st : (run ? TC_OK : TC_ETOOFEW);
+    if (b.out_flags) b.out_flags[bi] = flags;
   }
 }
 

@@ -79,10 +79,11 @@ def test_beam_step_workload(sampler, first_step, batch_index):
         assert (g["flat"][:, :2] < W.vocab).all()
 
 
-@pytest.mark.parametrize("top_k,nb", [(200, 2), (0, 1), (5, 4)])
-def test_beam_step_shapes(sampler, top_k, nb):
+@pytest.mark.parametrize("top_k,nb,top_p", [(200, 2, 0.8), (0, 1, 1.0), (5, 4, 0.8), (40, 3, 1.0), (100, 2, 1.0)])
+def test_beam_step_shapes(sampler, top_k, nb, top_p):
     # top-k 200: the general row path; top-k 0 with top-p 1: every finite score
-    # of a small vocabulary is live; 4 beams of top-k 5
+    # of a small vocabulary is live (700 joint entries, staged in LDS); 4 beams
+    # of top-k 5; 120 and 200 joint entries (two and four per lane)
     g_ = np.random.default_rng(top_k + nb)
     V = 8194 if top_k else 700
     batch = 6
@@ -92,7 +93,7 @@ def test_beam_step_shapes(sampler, top_k, nb):
     bonus = -g_.random(batch * nb) * 10
     n_draws = 2 * nb
     u = g_.random(batch * n_draws)
-    kw = _kw(top_k=top_k, top_p=0.8 if top_k else 1.0)
+    kw = _kw(top_k=top_k, top_p=top_p)
     g = _run(sampler, x, off, hist.reshape(-1), bonus, nb, u, n_draws, **kw)
     o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, off, hist.reshape(-1), bonus, nb, u, n_draws)
     _compare(g, o, "shapes", top_k=top_k, nb=nb)
@@ -133,3 +134,37 @@ def test_beam_step_rejects_bad_arguments(sampler):
     rc = L.tc_indextts_beam_step(sampler.ctx, ctypes.byref(p), x.data_ptr(), 0, 2, 0, 100, 100, None, None,
                                  b.data_ptr(), u.data_ptr(), 6, cf.data_ptr(), cs.data_ptr(), st.data_ptr(), None, s)
     assert rc == _lib.TC_EINVAL  # num_beams 0
+
+
+def test_beam_step_concentrated_refill(sampler):
+    # generation.rs:917-935 on logits: each beam row keeps two ids (top-k 2),
+    # the first step's beam scores are 0, -1e9, -1e9.  The active beam's two ids
+    # are drawn first; the inactive beams' ids (weights exactly 0 until then)
+    # refill the other four draws.
+    g_ = np.random.default_rng(21)
+    V, nb, batch = 500, 3, 8
+    x = (g_.standard_normal((batch * nb, V)) * 3).astype(np.float32)
+    bonus = np.array([0.0 if r % nb == 0 else -1e9 for r in range(batch * nb)])
+    u = g_.random(batch * 6)
+    kw = _kw(top_k=2, top_p=1.0, penalty=1.0)
+    g = _run(sampler, x, None, None, bonus, nb, u, 6, **kw)
+    o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, None, None, bonus, nb, u, 6)
+    assert (o["status"] == 0).all()
+    _compare(g, o, "refill")
+    assert (g["flat"][:, :2] < V).all() and all(len(set(r)) == 6 for r in g["flat"].tolist())
+
+
+def test_beam_step_boundary_draws_take_the_exact_path(sampler):
+    # four equal kept scores: weights 0.25 and a uniform of 0.5 put the target
+    # on a running sum exactly (acc > u fails at the second entry).  The draw
+    # falls inside the margin, runs the reference's sequential loops and is
+    # flagged; exp(0) = 1 is exact, so the candidates still equal the oracle's.
+    V, nb, batch = 64, 1, 4
+    x = np.full((batch, V), -30.0, np.float32)
+    x[:, [3, 17, 40, 41]] = 2.0
+    u = np.tile([0.5, 0.5, 0.25, 0.999], batch)
+    kw = _kw(top_k=4, top_p=1.0, penalty=1.0)
+    g = _run(sampler, x, None, None, np.zeros(batch), nb, u, 4, **kw)
+    o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, None, None, np.zeros(batch), nb, u, 4)
+    assert (g["flags"] & 16).all()
+    assert np.array_equal(g["flat"], o["flat"]) and np.array_equal(g["scores"], o["scores"])
