@@ -375,6 +375,29 @@ def test_cosy_random_rows_and_ras(sampler):
     assert ((g["flags"] & 2) != 0).sum() >= 4
 
 
+def test_cosy_fast_path_ties_eos_and_ras(sampler):
+    # logits on a 0.5 grid (many equal probabilities at the top_k-th rank: the
+    # reference's order is probability descending, id ascending), the
+    # ignore_eos id inside the candidate range, and rows whose dominant token
+    # is in the window (they draw from every probability)
+    g_ = np.random.default_rng(33)
+    V, rows, eos = 6564, 16, 100
+    x = (np.round(g_.standard_normal((rows, V)) * 6.0) / 2.0).astype(np.float32)
+    x[:, eos] = x.max(axis=1) + 1.0
+    hot = g_.integers(200, V, rows)
+    x[np.arange(rows), hot] = x.max(axis=1) + 6.0  # dominant: the nucleus is that one token
+    hist = [(g_.integers(0, V, 7).tolist() + [int(hot[r])] * (2 if r % 2 == 0 else 0)) for r in range(rows)]
+    u = g_.random(2 * rows).astype(np.float32)
+    g, o = run(sampler, O.COSY_RAS, x, hist, u, top_p=0.8, top_k=25, ras_win=10, ras_tau=0.1, eos_id=eos)
+    same(g, o)
+    assert ((g["flags"] & 2) != 0).sum() == rows // 2
+    # without the dominant token: the nucleus spans many tied ranks
+    x2 = (np.round(g_.standard_normal((rows, V)) * 4.0) / 2.0).astype(np.float32)
+    g, o = run(sampler, O.COSY_RAS, x2, hist, u, top_p=0.8, top_k=25, ras_win=10, ras_tau=0.1, eos_id=eos)
+    same(g, o)
+    assert (o["keep_count"] > 5).all()
+
+
 def test_cosy_invalid_params(sampler):
     x = np.zeros((1, 8), np.float32)
     with pytest.raises(_lib.TcError) as e:
