@@ -1719,6 +1719,7 @@ __device__ __forceinline__ void cosy_general(const RowArgs& a, CosyGenLds& G) {
 }
 
 struct CosyFastLds {
+  static constexpr int kWalk = 1024;
   uint32_t bins[64];  // thread maxima of d per 0.25-wide bucket below the row max
   float wmax[kMaxWaves];
   float wfin[kMaxWaves];
@@ -1726,7 +1727,101 @@ struct CosyFastLds {
   uint32_t out[4];
   SeqFastLds seq;
   FinLds fin;
+  float walk[kWalk];  // the repetition fallback's probabilities around the crossing
 };
+
+// random_sample_probs (llm.rs:594-604) from the fast path's registers: pv,
+// the exact probabilities of the thread's ITEMS elements from e0 (0 outside
+// the row and at the EOS id).  An approximate running sum A (thread, wave and
+// block scans) is within E = (V + 64) * 2^-24 * 1.01 * total of the
+// reference's sequential one, so the first index with pick < acc lies in
+// [first i with A + E > pick, first i with A - E > pick].  The exact
+// sequential sum up to the window is SeqSum over the probabilities before it
+// (exact terms; elements from the window on count as zeros), and one lane
+// walks the window.  Returns the token, or 0xffffffff when the window or the
+// list does not fit (then the caller's general walk decides).  Every thread
+// of the block calls it.
+template <int ITEMS>
+__device__ __forceinline__ uint32_t cosy_random_fast(const RowArgs& a, int row, const float (&pv)[ITEMS], int e0,
+                                                     CosyFastLds& F) {
+  const int t = threadIdx.x, V = a.V, lane = lane_id(), wv = wave_id(), nw = num_waves();
+  const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row + 1];
+  float pre[ITEMS];
+  float tp = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    tp += pv[i];
+    pre[i] = tp;
+  }
+  const float tinc = dpp_scan_f32(tp);
+  if (lane == kWave - 1) F.wmax[wv] = tinc;
+  lds_barrier();
+  float woff, wall;
+  wave_table_f32(F.wmax, &woff, &wall);
+  const float base = woff + (tinc - tp);
+  const float E = ((float)V + 64.0f) * 0x1p-24f * 1.01f * wall + 0x1p-60f;
+  uint32_t lo = 0xffffffffu, hi = 0xffffffffu;
+#pragma unroll
+  for (int i = ITEMS - 1; i >= 0; --i) {
+    const int e = e0 + i;
+    const float A = base + pre[i];
+    if (e >= 0 && e < V && A + E > pick) lo = (uint32_t)e;
+    if (e >= 0 && e < V && A - E > pick) hi = (uint32_t)e;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
+    lo = l2 < lo ? l2 : lo;
+    hi = h2 < hi ? h2 : hi;
+  }
+  if (lane == 0) {
+    F.wcand[wv] = lo;
+    F.bins[wv] = hi;
+  }
+  lds_barrier();
+  for (int w = 0; w < nw; ++w) {
+    lo = F.wcand[w] < lo ? F.wcand[w] : lo;
+    hi = F.bins[w] < hi ? F.bins[w] : hi;
+  }
+  if (lo == 0xffffffffu) return (uint32_t)(V - 1);  // no running sum can exceed pick
+  const uint32_t end = hi == 0xffffffffu ? (uint32_t)(V - 1) : hi;  // inclusive
+  if (end - lo + 1u > (uint32_t)CosyFastLds::kWalk) return 0xffffffffu;
+  // the exact sequential sum of the probabilities before the window
+  float ap[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) ap[i] = (e0 + i < (int)lo) ? pv[i] : 0.0f;
+  SeqSum<ITEMS> sq;
+  sq.predict(ap, F.seq);
+  lds_barrier();
+  sq.classify(ap, ~0u, 0u, e0, F.seq);
+  lds_barrier();  // write_list reads every wave's classification totals
+  const bool ok = sq.write_list(ap, ap, e0, F.seq, 0u, [](int) {});
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int e = e0 + i;
+    if (e >= (int)lo && e <= (int)end) F.walk[e - (int)lo] = pv[i];
+  }
+  lds_barrier();
+  if (ok) sq.replay_terms([](float v) { return v; }, F.seq);
+  lds_barrier();
+  if (wv == 0 && ok) sq.replay_walk(F.seq);
+  lds_barrier();
+  if (!ok || F.seq.bad) return 0xffffffffu;
+  if (t == 0) {
+    float acc = F.seq.S;
+    uint32_t found = (uint32_t)(V - 1);
+    for (uint32_t e = lo; e <= end; ++e) {
+      acc += F.walk[e - lo];
+      if (pick < acc) {
+        found = e;
+        break;
+      }
+    }
+    F.out[2] = found;
+  }
+  __syncthreads();
+  return F.out[2];
+}
 // The fast path hands a row to the general path before the general path
 // touches LDS, and uses the general path's arrays only after its own are done.
 union CosyLds {
@@ -1980,12 +2075,19 @@ __device__ __forceinline__ bool cosy_fast(const RowArgs& a, CosyLds& U) {
   const bool ras = F.out[1] != 0u;
   (void)top;
   if (ras) {
-    // random_sample_probs over every probability: exact terms for all
+    // random_sample_probs over every probability: exact terms for all (every
+    // lane active: the wave-cooperative expf)
     float pv[ITEMS];
 #pragma unroll
-    for (int i = 0; i < ITEMS; ++i) pv[i] = ((vm >> i) & 1u) ? expf_glibc(d[i]) / S : 0.0f;
-    __syncthreads();  // the general path's arrays overlay the fast path's
-    const uint32_t tok = cosy_random<ITEMS>(a, row, pv, valid_mask<ITEMS>(V, shift), e0, U.g);
+    for (int i = 0; i < ITEMS; ++i) {
+      const float e = expf_glibc_wave(((vm >> i) & 1u) ? d[i] : 0.0f);
+      pv[i] = ((vm >> i) & 1u) ? e / S : 0.0f;
+    }
+    uint32_t tok = cosy_random_fast<ITEMS>(a, row, pv, e0, F);
+    if (tok == 0xffffffffu) {
+      __syncthreads();  // the general path's arrays overlay the fast path's
+      tok = cosy_random<ITEMS>(a, row, pv, valid_mask<ITEMS>(V, shift), e0, U.g);
+    }
     finish_row(a, row, tok, TC_OK, TC_FLAG_RAS);
   }
   return true;

@@ -130,6 +130,21 @@ def test_cosy_workload_bit_exact(sampler, batch_index):
         assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
 
 
+@pytest.mark.parametrize("batch_index", [0, 1])
+def test_cosy_workload_every_window_fires(sampler, batch_index):
+    # tau 0: the threshold is 0, so every row draws from random_sample_probs
+    # (the full-row sequential CDF); ids bit-exact, every row flagged
+    w = synth.WORKLOADS["cosy-ras-128x6564"]
+    b = synth.make_batch(w, batch_index=batch_index)
+    g = G.run_gpu(sampler, w, b, CAP, ras_tau=0.0)
+    o = G.run_oracle(w, b, CAP, ras_tau=0.0)
+    assert (g["status"] == 0).all() and (o["status"] == 0).all()
+    mism = np.nonzero(g["ids"] != o["ids"])[0]
+    _report(w.name + " all-RAS", batch=batch_index, rows=w.rows, id_mismatch=len(mism))
+    assert len(mism) == 0, mism[:10]
+    assert ((g["flags"] & 2) != 0).all() and np.array_equal(g["flags"], o["flags"].astype(np.int32))
+
+
 def test_cosy_ras_rows_fire(sampler):
     w = synth.WORKLOADS["cosy-ras-128x6564"]
     b = synth.make_batch(w)
