@@ -377,6 +377,81 @@ __device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, ui
     e[q] = surv[q] ? t : 0.0f;
   }
   uint32_t flags = 0;
+  // ---- decisions from tree-ordered f32 sums first (no verification outputs):
+  // a prefix scan of at most 128 non-negative terms and its quotients stay
+  // within (n + 32) * 2^-22 of the reference's sequential running sums (a
+  // relative bound on values <= 1); a decision inside that margin goes to the
+  // reference's loops below.
+  if (!a.topk_count && !a.norm) {
+    bool ok = true;
+    uint32_t cut = ns;
+    if (a.do_topp) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        if (surv[q]) {
+          F.er[rk[q]] = e[q];
+          F.vr[rk[q]] = v[q];
+        }
+      lds_wait();
+      const float St = dpp_wave_sum(e[0] + e[1]);
+      float c[2];
+      float carry = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t r = (uint32_t)(q * kWave + lane);
+        const float pr = (q < NS && r < ns) ? F.er[r] / St : 0.0f;
+        c[q] = q < NS ? dpp_scan_f32(pr) + carry : 0.0f;
+        if (q < NS) carry = rl_f32(c[q], kWave - 1);
+      }
+      const float mg = (float)(ns + 32u) * 0x1p-22f;
+      const uint64_t over0 = __ballot((uint32_t)lane < ns && c[0] > a.top_p_f);
+      const uint64_t over1 = __ballot((uint32_t)(kWave + lane) < ns && c[1] > a.top_p_f);
+      const uint32_t r = over0 ? (uint32_t)__builtin_ctzll(over0) : (over1 ? 64u + (uint32_t)__builtin_ctzll(over1) : ns);
+      // the running sums at the cut and just before it against p
+      const float c_at = r < ns ? rl_f32(r < 64u ? c[0] : c[1], (int)(r & 63u)) : 0.0f;
+      const uint32_t rp = r < ns ? r : ns;  // the last position below the cut is rp - 1
+      const float c_prev = rp ? rl_f32(rp - 1u < 64u ? c[0] : c[1], (int)((rp - 1u) & 63u)) : 0.0f;
+      ok = (r >= ns || c_at - a.top_p_f > mg) && (rp == 0u || a.top_p_f - c_prev > mg);
+      cut = r < ns ? r + 1u : ns;
+      if (ok && cut < ns && F.vr[cut - 1u] == F.vr[cut]) flags |= TC_FLAG_TIE_CUT;
+    }
+    if (ok) {
+      bool kp[2];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) kp[q] = surv[q] && rk[q] < cut;
+      const float S2t = dpp_wave_sum((kp[0] ? e[0] : 0.0f) + (kp[1] ? e[1] : 0.0f));
+      const uint64_t km0 = __ballot(kp[0]), km1 = __ballot(kp[1]);
+      const uint32_t nk = (uint32_t)(__popcll(km0) + __popcll(km1));
+      const float c0 = dpp_scan_f32(kp[0] ? e[0] / S2t : 0.0f);
+      const float c1 = NS == 2 ? dpp_scan_f32(kp[1] ? e[1] / S2t : 0.0f) + rl_f32(c0, kWave - 1) : 0.0f;
+      const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+      const float mg = (float)(nk + 32u) * 0x1p-22f;
+      uint32_t tok = 0;
+      if (u > 0.0f) {
+        // the first kept entry whose running sum reaches u, else 0
+        const uint64_t h0 = __ballot(kp[0] && c0 >= u), h1 = __ballot(kp[1] && c1 >= u);
+        uint32_t pk = 0xffffffffu;
+        if (h0) pk = (uint32_t)__builtin_ctzll(h0);
+        else if (h1) pk = 64u + (uint32_t)__builtin_ctzll(h1);
+        // the kept entry before it (or the last kept one when none reaches u)
+        uint64_t b0 = km0, b1 = km1;
+        if (pk != 0xffffffffu) {
+          b0 = pk < 64u ? (km0 & ((1ull << pk) - 1ull)) : km0;
+          b1 = pk < 64u ? 0ull : (km1 & ((1ull << (pk - 64u)) - 1ull));
+        }
+        const uint32_t pv = b1 ? 64u + 63u - (uint32_t)__builtin_clzll(b1) : (b0 ? 63u - (uint32_t)__builtin_clzll(b0) : 0xffffffffu);
+        const float c_pk = pk != 0xffffffffu ? rl_f32(pk < 64u ? c0 : c1, (int)(pk & 63u)) : 0.0f;
+        const float c_pv = pv != 0xffffffffu ? rl_f32(pv < 64u ? c0 : c1, (int)(pv & 63u)) : 0.0f;
+        ok = (pk == 0xffffffffu || c_pk - u > mg) && (pv == 0xffffffffu || u - c_pv > mg);
+        if (pk != 0xffffffffu) tok = rl_u32(pk < 64u ? id[0] : id[1], (int)(pk & 63u));
+      }
+      if (ok) {
+        if (lane == 0) put_result(a, row, tok, TC_OK, flags);
+        return;
+      }
+    }
+    flags = 0;
+  }
   bool kept[2] = {surv[0], surv[1]};
   if (a.do_topp) {
     // top-p (255-299): survivors occupy ranks [0, ns)

@@ -59,6 +59,29 @@ def test_qwen_workloads_bit_exact(sampler, name, batch_index):
         assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
 
 
+@pytest.mark.parametrize("name", ["qwen-talker-1x3072", "qwen-cp-512x2048"])
+@pytest.mark.parametrize("batch_index", [0, 1, 2, 3, 4, 5])
+def test_qwen_workload_ids_without_verification(sampler, name, batch_index):
+    # without verification outputs the kernel decides top-p and the draw from
+    # tree-ordered f32 sums first (the reference's loops only inside the
+    # margin): the same ids and flags as the oracle and the verifying launch
+    w = synth.WORKLOADS[name]
+    b = synth.make_batch(w, batch_index=batch_index)
+    logits, ho, hi, un = G.to_dev(b, w)
+    r = sampler.sample(G.params_for(w, "gpu"), logits, ho, hi, un, verify_cap=0)
+    torch.cuda.synchronize()
+    ids = r.ids.cpu().numpy().view(np.uint32)
+    o = G.run_oracle(w, b, CAP)
+    amb = (o["flags"] & 1) != 0
+    mism = np.nonzero((ids != o["ids"]) & ~amb)[0]
+    _report(name + " no-verify", batch=batch_index, rows=w.rows, id_mismatch=len(mism))
+    assert (r.status.cpu().numpy() == 0).all()
+    assert len(mism) == 0, mism[:10]
+    assert np.array_equal(r.flags.cpu().numpy(), o["flags"].astype(np.int32))
+    gv = G.run_gpu(sampler, w, b, CAP)
+    assert np.array_equal(ids, gv["ids"])
+
+
 @pytest.mark.parametrize("batch_index", [0, 1, 2])
 def test_indextts_workload_bit_exact(sampler, batch_index):
     # the log_softmax denominator is the reference's sequential f32 sum, its log
