@@ -192,15 +192,21 @@ struct SeqSum {
                      (P0 + D) * (m_hi + 0x1p-20f) < __uint_as_float(eb0 + 0x00800000u);
     ulp0 = 0.0f;
     T = D;
-    if (__ballot(!uni) == 0ull) {
-      ulp0 = __uint_as_float(eb0 - 0x0b800000u);
+    const uint64_t nub = __ballot(!uni);
+    if (__popcll(nub) <= 16) {
+      // the short form; a thread whose range may cross a binade (those near a
+      // crossing of the running sum, at most 16 per wave here) lists every
+      // element instead, r = 0 (scale 0), and the replay classifies them again
+      // against the refined prediction
+      ulp0 = uni ? __uint_as_float(eb0 - 0x0b800000u) : 0.0f;
+      if (!uni) unsafe = (1u << ITEMS) - 1u;
       // r = round-half-even(t / 2^(e-23)) is read from the bits of the f32 sum
       // 2^23 + t * 2^(23-e) (2^23 plus that integer; 2^24 reads as 2^23).  The
       // exact term lies strictly between ap * (1 -+ 2^-20) after the product's
       // own rounding (kSeqErr is 2^-21), so both ends giving the same bits
       // settle the rounding; a tie always lies between ends that differ.  The
       // range stays below 2^e, so t * 2^(23-e) < 2^23.
-      const float scale = __uint_as_float(0x8a800000u - eb0);  // 2^(23-e)
+      const float scale = uni ? __uint_as_float(0x8a800000u - eb0) : 0.0f;  // 2^(23-e)
       const float c_lo = scale * (1.0f - 2.0f * kSeqErr), c_hi = scale * (1.0f + 2.0f * kSeqErr);
       uint32_t dif = 0;
 #pragma unroll
