@@ -1269,6 +1269,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 //    reference's sequential sums; the first index whose running sum reaches u.
 constexpr int kLargeThreads = 1024;
 constexpr int kLargeCand = 2048;
+constexpr int kLargeU = 4;  // 16-byte chunks in flight per thread in the streaming passes
 constexpr int kLargePer = kLargeCand / kLargeThreads;  // candidate slots per thread
 constexpr int kLargeVocab = 262144;
 constexpr int kLargeWords = kLargeVocab / 32;
@@ -1335,11 +1336,10 @@ struct LChunk {
   uint32_t sn;  // bit h: in the history or the EOS id
   bool bad;
 };
-__device__ __forceinline__ LChunk load_lchunk(const uint4* base, int q, int shift, int V, const uint32_t* bits,
-                                              int nwords, int eos) {
+__device__ __forceinline__ LChunk decode_lchunk(const uint4 v, int q, int shift, int V, const uint32_t* bits,
+                                                int nwords, int eos) {
   LChunk c;
   const int e0 = q * 8 - shift;
-  const uint4 v = base[q];
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   const uint32_t hb = bits_at_fn(bits, nwords, e0);
   c.bad = false;
@@ -1353,6 +1353,47 @@ __device__ __forceinline__ LChunk load_lchunk(const uint4* base, int q, int shif
     c.x[h] = in ? __uint_as_float(b) : -3.3895313892515355e38f;
     const bool s = ((hb >> h) & 1u) != 0u || e == eos;
     c.sn |= (s ? 1u : 0u) << h;
+  }
+  return c;
+}
+
+__device__ __forceinline__ uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+// ckey(x) >> 16 for the f32 widening of a bf16 value b (both zeros give 0x8000)
+__device__ __forceinline__ uint32_t bkey16(uint32_t b) {
+  const uint32_t k = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (b & 0x7fffu) ? k : 0x8000u;
+}
+
+// The integer view of a chunk for the streaming passes: the bf16 bits of its 8
+// values, their keys, which are live (inside the row, not in the history, not
+// the EOS id), which are penalised (inside the row, in the history, not the
+// EOS id), and whether a value inside the row is non-finite.
+struct KChunk {
+  uint32_t b[8];
+  uint32_t k[8];
+  uint32_t live, pen;
+  bool bad;
+};
+__device__ __forceinline__ KChunk key_chunk(const uint4 v, int q, int shift, int V, const uint32_t* bits, int nwords,
+                                            int eos) {
+  KChunk c;
+  const int e0 = q * 8 - shift;  // in [-7, V): q < nchunks
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t hb = bits_at_fn(bits, nwords, e0) & 0xffu;
+  uint32_t inm = 0xffu;
+  if (e0 < 0) inm &= 0xffu << (uint32_t)(-e0);
+  if (e0 + 8 > V) inm &= (1u << (uint32_t)(V - e0)) - 1u;
+  const uint32_t em = (eos >= e0 && eos < e0 + 8) ? 1u << (uint32_t)(eos - e0) : 0u;
+  c.live = inm & ~hb & ~em;
+  c.pen = inm & hb & ~em;
+  c.bad = false;
+#pragma unroll
+  for (int h = 0; h < 8; ++h) {
+    const uint32_t b = (h & 1) ? (w[h >> 1] >> 16) : (w[h >> 1] & 0xffffu);
+    c.b[h] = b;
+    c.bad |= ((inm >> h) & 1u) && (b & 0x7f80u) == 0x7f80u;
+    c.k[h] = bkey16(b);
   }
   return c;
 }
@@ -1388,21 +1429,54 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     if (a.do_temp) v = v * a.tmul + 0.0f;
     return v;
   };
+  // Each streaming pass keeps kLargeU 16-byte loads in flight per thread (one
+  // at a time leaves the pass bound by load latency, not by HBM).
+  const int bd = (int)blockDim.x;
   // pass A
   uint32_t bad = 0, kmax = 0;
   uint64_t best = 0;
-  for (int q = t; q < nchunks; q += blockDim.x) {
-    const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
-    bad |= c.bad ? 1u : 0u;
+  if (a.greedy) {
+    uint4 raw[kLargeU], nxt[kLargeU];
 #pragma unroll
-    for (int h = 0; h < 8; ++h) {
-      const int e = q * 8 - shift + h;
-      if (a.greedy) {
-        const uint64_t k = ((uint64_t)ckey(logit(c.x[h], (c.sn >> h) & 1u, e)) << 32) | (uint64_t)(~(uint32_t)e);
-        best = (e >= 0 && e < V && k > best) ? k : best;
+    for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
+    for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(q0 + (kLargeU + u) * bd, nchunks - 1)];
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = q0 + u * bd;
+        if (q >= nchunks) break;
+        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+        bad |= c.bad ? 1u : 0u;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int e = q * 8 - shift + h;
+          const uint64_t k = ((uint64_t)ckey(logit(c.x[h], (c.sn >> h) & 1u, e)) << 32) | (uint64_t)(~(uint32_t)e);
+          best = (e >= 0 && e < V && k > best) ? k : best;
+        }
       }
-      const uint32_t k16 = ckey(c.x[h]) >> 16;
-      kmax = (!((c.sn >> h) & 1u) && k16 > kmax) ? k16 : kmax;
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
+    }
+  } else {
+    // the largest key outside the history, from the bf16 bits alone
+    uint4 raw[kLargeU], nxt[kLargeU];
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
+    for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(q0 + (kLargeU + u) * bd, nchunks - 1)];
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = q0 + u * bd;
+        if (q >= nchunks) break;
+        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
+        bad |= c.bad ? 1u : 0u;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) kmax = (((c.live >> h) & 1u) && c.k[h] > kmax) ? c.k[h] : kmax;
+      }
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
   }
   bad = block_or_u(bad, S.s);
@@ -1429,12 +1503,26 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   }
   kmax = block_max_u(kmax, S.s);
   // pass B: exact histogram of the 256 keys at and below the largest
-  for (int q = t; q < nchunks; q += blockDim.x) {
-    const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
+  {
+    uint4 raw[kLargeU], nxt[kLargeU];
 #pragma unroll
-    for (int h = 0; h < 8; ++h) {
-      const uint32_t dk = kmax - (ckey(c.x[h]) >> 16);
-      if (!((c.sn >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
+    for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
+    for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(q0 + (kLargeU + u) * bd, nchunks - 1)];
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = q0 + u * bd;
+        if (q >= nchunks) break;
+        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const uint32_t dk = kmax - c.k[h];
+          if (((c.live >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
   }
   __syncthreads();
@@ -1461,25 +1549,37 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const uint32_t keyK = kmax - bK;
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
   const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
-  // pass C: candidates in vocabulary order, a tile of blockDim chunks at a time
+  // pass C: candidates in vocabulary order, a tile of kLargeU * blockDim
+  // chunks at a time, thread t holding the tile's chunks kLargeU * t + u
+  // The next tile's loads are issued before this tile's barrier.
   uint32_t n_c = 0;
   int parity = 0;
-  for (int tb = 0; tb < nchunks; tb += blockDim.x, parity ^= 1) {
-    const int q = tb + t;
-    uint32_t sel = 0;
-    float v[8];
-    if (q < nchunks) {
-      const LChunk c = load_lchunk(base, q, shift, V, S.bits, nwords, eos);
+  uint4 raw[kLargeU], nxt[kLargeU];
 #pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const int e = q * 8 - shift + h;
-        const bool sn = (c.sn >> h) & 1u;
-        v[h] = logit(c.x[h], sn, e);
-        const bool ok = e >= 0 && e < V && (sn ? v[h] >= thr : (ckey(c.x[h]) >> 16) >= keyK);
-        sel |= (ok ? 1u : 0u) << h;
+  for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(kLargeU * t + u, nchunks - 1)];
+  for (int tb = 0; tb < nchunks; tb += kLargeU * bd, parity ^= 1) {
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + kLargeU * bd + kLargeU * t + u, nchunks - 1)];
+    // selected: live ids whose key reaches keyK, penalised ids whose logit
+    // reaches thr (the EOS id's logit is -inf: never); no branches per element
+    uint64_t sel = 0, pens = 0;  // bit 8u + h
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) {
+      const int q = tb + kLargeU * t + u;
+      if (q < nchunks) {
+        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const float x = __uint_as_float(c.b[h] << 16);
+          float vp = x * (x > 0.0f ? a.inv_pen : a.pen_f);
+          vp = a.do_temp ? vp * a.tmul + 0.0f : vp;
+          const bool ok = ((c.live >> h) & 1u) ? c.k[h] >= keyK : (((c.pen >> h) & 1u) != 0u && vp >= thr);
+          sel |= (ok ? 1ull : 0ull) << (8 * u + h);
+        }
+        pens |= (uint64_t)c.pen << (8 * u);
       }
     }
-    const uint32_t cnt = (uint32_t)__builtin_popcount(sel);
+    const uint32_t cnt = (uint32_t)__popcll(sel);
     const uint32_t ci = dpp_scan_u32(cnt);
     if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
     __syncthreads();
@@ -1491,15 +1591,25 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     }
     if (sel && n_c + tile <= (uint32_t)kLargeCand) {
 #pragma unroll
-      for (int h = 0; h < 8; ++h)
-        if ((sel >> h) & 1u) {
-          const uint64_t kv = ((uint64_t)(~ckey(v[h])) << 32) | (uint32_t)(q * 8 - shift + h);
-          S.cand[off] = kv;
-          S.candv[off] = kv;
-          ++off;
-        }
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = tb + kLargeU * t + u;
+#pragma unroll
+        for (int h = 0; h < 8; ++h)
+          if ((sel >> (8 * u + h)) & 1ull) {
+            const int e = q * 8 - shift + h;
+            const uint32_t wv = u4_word(raw[u], h >> 1);
+            const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
+            const float vv = logit(__uint_as_float(b), ((pens >> (8 * u + h)) & 1ull) != 0ull, e);
+            const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
+            S.cand[off] = kv;
+            S.candv[off] = kv;
+            ++off;
+          }
+      }
     }
     n_c += tile;
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
   }
   __syncthreads();
   if (n_c > (uint32_t)kLargeCand) {
