@@ -168,3 +168,24 @@ def test_beam_step_boundary_draws_take_the_exact_path(sampler):
     o = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), x, None, None, np.zeros(batch), nb, u, 4)
     assert (g["flags"] & 16).all()
     assert np.array_equal(g["flat"], o["flat"]) and np.array_equal(g["scores"], o["scores"])
+
+
+def test_beam_step_bf16_rows(sampler):
+    # bf16 logits are widened exactly (to_dtype(F32)); the oracle sees the same values
+    from talechime_amd.synth import bf16_bits_to_f32, to_bf16_bits
+    from talechime_amd.sampler import make_params
+    g_ = np.random.default_rng(5)
+    V, nb, batch = 8194, 3, 8
+    x = (g_.standard_normal((batch * nb, V)) * 4).astype(np.float32)
+    bits = to_bf16_bits(x)
+    xf = bf16_bits_to_f32(bits)
+    bonus = -g_.random(batch * nb) * 20
+    u = g_.random(batch * 6)
+    p = make_params(_lib.INDEXTTS, **_kw(penalty=1.0))
+    r = sampler.beam_step(p, torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda(), None, None,
+                          torch.from_numpy(bonus).cuda(), nb, torch.from_numpy(u).cuda())
+    torch.cuda.synchronize()
+    g = {"flat": r.flat.cpu().numpy().view(np.uint32), "scores": r.scores.cpu().numpy(),
+         "status": r.status.cpu().numpy(), "flags": r.flags.cpu().numpy()}
+    o = O.idx_beam_step(O.make_params(O.INDEXTTS, **_kw(penalty=1.0)), xf, None, None, bonus, nb, u, 6)
+    _compare(g, o, "bf16")

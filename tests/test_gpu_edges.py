@@ -401,6 +401,37 @@ def test_cosy_fast_path_ties_eos_and_ras(sampler):
     assert (o["keep_count"] > 5).all()
 
 
+@pytest.mark.parametrize("V,top_k,bf16", [(300, 1, False), (2048, 64, False), (6564, 25, True), (16000, 40, False),
+                                          (6761, 25, False)])
+def test_cosy_fast_path_shapes(sampler, V, top_k, bf16):
+    # the fast path across vocabularies, top_k at both ends of its range, bf16
+    # rows, the EOS id inside the row and windows that fire on every other row
+    g_ = np.random.default_rng(V + top_k)
+    rows = 12
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    hot = g_.integers(0, V, rows)
+    x[np.arange(rows), hot] = x.max(axis=1) + 5.0
+    eos = int(g_.integers(0, V))
+    hist = [g_.integers(0, V, 9).tolist() + ([int(hot[r])] if r % 2 else []) for r in range(rows)]
+    u = g_.random(2 * rows).astype(np.float32)
+    g, o = run(sampler, O.COSY_RAS, x, hist, u, bf16=bf16, ld_pad=5, top_p=0.8, top_k=top_k, ras_win=10, ras_tau=0.1,
+               eos_id=eos)
+    same(g, o)
+    assert np.array_equal(g["flags"], o["flags"].astype(np.int32))
+
+
+def test_qwen_fast_path_extreme_uniforms(sampler):
+    # u = 0 (token 0), u = 1 (reachable: the running sum may never reach it,
+    # then token 0) and u next to 1, on the fast path with and without top-p
+    g_ = np.random.default_rng(77)
+    V, rows = 3072, 6
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    u = np.array([0.0, 1.0, np.nextafter(np.float32(1.0), np.float32(0.0)), 0.5, 1.0, 0.0], np.float32)
+    for tp in (0.8, 1.0):
+        g, o = run(sampler, O.QWEN, x, None, u, temperature=0.9, top_k=50, top_p=tp)
+        same(g, o)
+
+
 def test_cosy_invalid_params(sampler):
     x = np.zeros((1, 8), np.float32)
     with pytest.raises(_lib.TcError) as e:
