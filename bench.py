@@ -139,6 +139,17 @@ def beam_bench(args):
         print(f"bench.py: {int((st != 0).sum())} beam elements returned a non-OK status", file=sys.stderr)
         sys.exit(1)
     sampler.close()
+    # algorithmic bytes per step: every beam row's logits and history, its beam
+    # score, the element's uniforms, and the candidates written (flat u32 + f64)
+    n_draws = 2 * nb
+    step_bytes = rows * (w.vocab * 4 + w.hist_len * 4 + 8) + B * n_draws * (8 + 4 + 8) + B * 8
+    achieved = step_bytes / (ms * 1e-3) / 1e9
+    extra = {"roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                          "algorithmic_bytes_per_step": step_bytes,
+                          "note": "latency-bound: two launches per step (row pass, joint draws); the joint draws move a few KB"}}
+    if not args.no_cpu:
+        extra["cpu_baseline"] = beam_cpu_baseline(w, bb, nb, args.cpu_seconds)
     print(json.dumps({
         "metric": f"indextts beam-sample steps/sec ({B} elements x {nb} beams x {w.vocab}, 6 draws)",
         "value": round(1e3 / ms, 1), "unit": "steps/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
@@ -147,7 +158,26 @@ def beam_bench(args):
         "config": {"workload": f"indextts-beam-{B}x{nb}x{w.vocab}", "elements": B, "num_beams": nb,
                    "n_draws": 2 * nb, "pool_batches": n_pool},
         "timing": f"{replays} replays of a HIP graph of {n_pool} steps (row pass + joint draws each)",
+        **extra,
     }), flush=True)
+
+
+def beam_cpu_baseline(w, bb, nb, seconds: float):
+    """The oracle's beam step (C restatement of generation.rs:640-701) on this host."""
+    from oracle import oracle as O
+
+    p = O.make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
+                      min_keep=w.min_keep)
+    args = (bb.logits, bb.hist_off, bb.hist_ids, bb.beam_scores, nb, bb.uniforms, 2 * nb)
+    O.idx_beam_step(p, *args)
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.idx_beam_step(p, *args)
+        done += 1
+    dt = time.perf_counter() - t0
+    B = bb.logits.shape[0] // nb
+    return {"value": round(done / dt, 2), "unit": "steps/s", "cores": 1, "kind": "port",
+            "sample": f"{done} steps of {B} elements x {nb} beams x {w.vocab}, single thread, {dt:.1f} s"}
 
 
 def main():
