@@ -214,10 +214,12 @@ __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
 // the first index whose running sum reaches u is the token (0 when u <= 0 or
 // none does).  Verification outputs: the first `cap` survivors in vocabulary
 // order with their probabilities.
+// surv: the ids the draw runs over (n of them); tk: the top-k survivors for
+// the verification outputs.
 template <int ITEMS>
-__device__ __forceinline__ void qwen_wide_cdf(const RowArgs& a, const float (&x)[ITEMS], uint32_t surv, uint32_t vm,
-                                              int e0, uint32_t n, uint32_t flags, SurvLds& sv, BlockScratch& s,
-                                              SeqLds& sq, ScanLds& sc) {
+__device__ __forceinline__ void qwen_wide_cdf(const RowArgs& a, const float (&x)[ITEMS], uint32_t surv, uint32_t tk,
+                                              uint32_t vm, int e0, uint32_t n, uint32_t flags, SurvLds& sv,
+                                              BlockScratch& s, SeqLds& sq, ScanLds& sc) {
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
   float* stage = reinterpret_cast<float*>(&sv);  // the survivor stage is not in use here
   constexpr int kStage = (int)(sizeof(SurvLds) / sizeof(float));
@@ -284,17 +286,20 @@ __device__ __forceinline__ void qwen_wide_cdf(const RowArgs& a, const float (&x)
   put_norm(a, row, S2);
   if (a.topk_count || a.keep_count) {
     uint32_t tot;
-    const uint32_t pos0 = block_excl_scan((uint32_t)__builtin_popcount(surv), s, &tot);
-    uint32_t p = pos0;
+    uint32_t p = block_excl_scan((uint32_t)__builtin_popcount(tk), s, &tot);
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((tk >> i) & 1u) {
+        if (p < a.cap && a.topk_count) a.topk_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
+        ++p;
+      }
+    p = block_excl_scan((uint32_t)__builtin_popcount(surv), s, &tot);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
       if ((surv >> i) & 1u) {
-        if (p < a.cap) {
-          if (a.topk_count) a.topk_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
-          if (a.keep_count) {
-            a.keep_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
-            a.keep_probs[(size_t)row * a.cap + p] = pv[i];
-          }
+        if (p < a.cap && a.keep_count) {
+          a.keep_ids[(size_t)row * a.cap + p] = (uint32_t)(e0 + i);
+          a.keep_probs[(size_t)row * a.cap + p] = pv[i];
         }
         ++p;
       }
@@ -648,6 +653,131 @@ __device__ __forceinline__ bool qwen_fast(const RowArgs& a, QFastLds& F) {
   return true;
 }
 
+// ================================================================ qwen, top-p over many survivors
+// The general path's LDS: the history map and the survivor stage, or, past
+// them, the rank sort of up to kWideCap survivors.
+constexpr int kWideCap = 4096;
+struct QGenLds {
+  uint8_t seen[kMaxVocabReg];
+  SurvLds sv;
+};
+union QGenU {
+  QGenLds g;
+  uint64_t wide[kWideCap];
+};
+static_assert(sizeof(uint64_t) * kWideCap <= sizeof(QGenLds), "the rank sort fits the general path's LDS");
+
+// top-p (sampling.rs:255-299) over kSurvCap < n <= kWideCap survivors (top-k
+// off or wide), then softmax and the draw (302-328) by qwen_wide_cdf over the
+// kept ones.  Every survivor is sorted into rank order (value descending, id
+// ascending; the reference's unstable sort leaves ties open: TC_FLAG_TIE_CUT
+// where they straddle the cut); thread t then holds ranks ITEMS * t + i (n <=
+// V <= ITEMS * blockDim), so the sequential f32 denominator in rank order and
+// the running sum of e / S are block_seqsum and seq_prefix over those
+// positions; the cut follows the first running sum above p (the crossing
+// rank kept).
+template <int ITEMS>
+__device__ __forceinline__ void qwen_wide_topp(const RowArgs& a, const float (&x)[ITEMS], uint32_t surv, uint32_t vm,
+                                               int e0, uint32_t n, uint32_t flags, QGenU& U, BlockScratch& s,
+                                               uint32_t* s_out, SeqLds& sq, ScanLds& sc) {
+  const int t = threadIdx.x;
+  // the survivors' rank keys, compacted in vocabulary order, padded, sorted
+  uint32_t tot;
+  uint32_t pos = block_excl_scan((uint32_t)__builtin_popcount(surv), s, &tot);
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((surv >> i) & 1u) U.wide[pos++] = ((uint64_t)(~ckey(x[i])) << 32) | (uint32_t)(e0 + i);
+  const int n_pad = next_pow2((int)n < 2 ? 2 : (int)n);
+  for (int j = (int)n + t; j < n_pad; j += blockDim.x) U.wide[j] = ~0ull;
+  __syncthreads();
+  block_bitonic_sort(U.wide, n_pad);
+  // ranks ITEMS * t + i in registers
+  const int p0 = ITEMS * t;
+  float v[ITEMS], e[ITEMS];
+  uint32_t id[ITEMS];
+  const float vmax = untkey(~(uint32_t)(U.wide[0] >> 32));
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const bool in = p0 + i < (int)n;
+    const uint64_t kv = in ? U.wide[p0 + i] : 0ull;
+    v[i] = in ? untkey(~(uint32_t)(kv >> 32)) : 0.0f;
+    id[i] = (uint32_t)kv;
+    e[i] = in ? expf_glibc(v[i] - vmax) : 0.0f;
+  }
+  __syncthreads();  // the sort buffer is free from here
+  float* stage = reinterpret_cast<float*>(U.wide);
+  auto same = [](float y) { return y; };
+  float S;
+  {
+    SeqThread<ITEMS> th;
+    if (!block_seqsum<ITEMS>(e, ~0u, e, same, p0, 0, th, sq, sc, &S))
+      S = block_seqsum_slow<ITEMS>(e, p0, (int)n, stage, kWideCap * 2, &sq.S);
+  }
+  float q[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) q[i] = p0 + i < (int)n ? e[i] / S : 0.0f;
+  // the running sum of q in rank order: the first rank above p
+  uint32_t first = 0xffffffffu;
+  {
+    SeqThread<ITEMS> th;
+    float Sq;
+    if (block_seqsum<ITEMS>(q, ~0u, q, same, p0, 0, th, sq, sc, &Sq)) {
+      float pre[ITEMS];
+      seq_prefix<ITEMS>(th, sq, pre);
+#pragma unroll
+      for (int i = ITEMS - 1; i >= 0; --i)
+        if (p0 + i < (int)n && pre[i] > a.top_p_f) first = (uint32_t)(p0 + i);
+      first = block_min_u(first, s);
+    } else {
+      // one lane walks the running sum
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+        if (p0 + i < (int)n) stage[p0 + i] = q[i];
+      __syncthreads();
+      if (t == 0) {
+        float cum = 0.0f;
+        uint32_t f = 0xffffffffu;
+        for (uint32_t r = 0; r < n; ++r) {
+          cum += stage[r];
+          if (cum > a.top_p_f) {
+            f = r;
+            break;
+          }
+        }
+        s_out[2] = f;
+      }
+      __syncthreads();
+      first = s_out[2];
+    }
+  }
+  const uint32_t cut = first != 0xffffffffu ? first + 1u : n;
+  // equal values straddling the cut: the reference's unstable order decides
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if ((uint32_t)(p0 + i) + 1u == cut) s_out[2] = f2u(v[i]);
+    if ((uint32_t)(p0 + i) == cut) s_out[3] = f2u(v[i]);
+  }
+  // the kept ids (ranks below the cut) as a bitmap over the vocabulary
+  uint32_t* bm = reinterpret_cast<uint32_t*>(U.wide);
+  const int nwords = (a.V + 31) >> 5;
+  for (int w = t; w < nwords; w += blockDim.x) bm[w] = 0u;
+  __syncthreads();
+  if (cut < n && s_out[2] == s_out[3]) flags |= TC_FLAG_TIE_CUT;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((uint32_t)(p0 + i) < cut) atomicOr(&bm[id[i] >> 5], 1u << (id[i] & 31u));
+  __syncthreads();
+  uint32_t kept = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const int el = e0 + i;
+    if (((surv >> i) & 1u) && ((bm[el >> 5] >> (el & 31)) & 1u)) kept |= 1u << i;
+  }
+  __syncthreads();  // the bitmap shares LDS with the CDF's staging
+  qwen_wide_cdf<ITEMS>(a, x, kept, surv, vm, e0, cut, flags, U.g.sv, s, sq, sc);
+}
+
 // ================================================================ qwen
 template <typename InT, int ITEMS>
 __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
@@ -656,8 +786,9 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
     if (qwen_fast<InT, ITEMS>(a, qf)) return;
     __syncthreads();
   }
-  __shared__ uint8_t s_seen[kMaxVocabReg];
-  __shared__ SurvLds sv;
+  __shared__ QGenU U;
+  uint8_t* s_seen = U.g.seen;
+  SurvLds& sv = U.g.sv;
   __shared__ uint32_t s_hist[256];
   __shared__ BlockScratch s;
   __shared__ uint32_t s_out[4];
@@ -747,10 +878,14 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
   write_topk(a, row, sv, n);
   if (n > (uint32_t)kSurvCap) {
     if (!a.do_topp) {
-      qwen_wide_cdf<ITEMS>(a, x, surv, vm, e0, n, flags, sv, s, qsq, qsc);
+      qwen_wide_cdf<ITEMS>(a, x, surv, surv, vm, e0, n, flags, sv, s, qsq, qsc);
       return;
     }
-    // top-p over more survivors than the LDS stage holds: not handled
+    if (n <= (uint32_t)kWideCap) {
+      qwen_wide_topp<ITEMS>(a, x, surv, vm, e0, n, flags, U, s, s_out, qsq, qsc);
+      return;
+    }
+    // top-p over more survivors than the rank sort holds: not handled
     finish_row(a, row, 0u, TC_EUNSUPPORTED, flags);
     if (t == 0 && a.keep_count) a.keep_count[row] = 0;
     put_norm(a, row, __builtin_nanf(""));

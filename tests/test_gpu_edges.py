@@ -176,7 +176,8 @@ def test_qwen_fast_path_and_fallback_distributions(sampler):
 def test_qwen_many_survivors_without_top_p(sampler):
     """top-k off (or wider than 1024) and top-p off: softmax and CDF over every
     survivor of the register-resident row, bit-exact with the verification
-    outputs; top-p over that many survivors still reports TC_EUNSUPPORTED."""
+    outputs; top-p over up to 4096 survivors runs the rank sort, beyond that it
+    reports TC_EUNSUPPORTED."""
     g_ = np.random.default_rng(31)
     for V in (3072, 8194, 16000):
         x = (g_.standard_normal((6, V)) * 2).astype(np.float32)
@@ -189,9 +190,29 @@ def test_qwen_many_survivors_without_top_p(sampler):
             g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.8, top_k=k, top_p=1.0, penalty=1.1)
             same(g, o)
         g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.8, top_k=0, top_p=0.9, penalty=1.1)
-        wide = o["topk_count"] > KSURV
+        wide = o["topk_count"] > 4096
         assert (g["status"][wide] == _lib.TC_EUNSUPPORTED).all()
-        same(g, o, rows=np.nonzero(~wide)[0])
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=np.nonzero(~wide & ~tie)[0])
+
+
+@pytest.mark.parametrize("V,k", [(3072, 0), (2048, 0), (4096, 2000), (3072, 3072)])
+def test_qwen_top_p_over_many_survivors(sampler, V, k):
+    # top-k off or wide, top-p on: every survivor sorted into rank order, the
+    # denominator and the running sum as the reference's sequential f32 sums
+    g_ = np.random.default_rng(V + k)
+    rows = 10
+    x = (g_.standard_normal((rows, V)) * 1.5).astype(np.float32)
+    x[1, g_.integers(0, V, V // 3)] = NEG
+    x[2] = np.round(x[2] * 2) / 2  # many equal values
+    hist = [g_.integers(0, V, 64).tolist() for _ in range(rows)]
+    u = g_.random(rows).astype(np.float32)
+    for tp in (0.5, 0.9, 0.99):
+        g, o = run(sampler, O.QWEN, x, hist, u, temperature=0.9, top_k=k, top_p=tp, penalty=1.1)
+        assert (o["topk_count"] > 1024).any()
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=np.nonzero(~tie)[0])
+        assert np.array_equal(g["flags"], o["flags"].astype(np.int32))
 
 
 def test_qwen_ties_and_degenerate_rows(sampler):
