@@ -183,7 +183,7 @@ def beam_cpu_baseline(w, bb, nb, seconds: float):
 def main():
     args = parse()
     if args.gpus != 1:
-        print("bench.py: this sampler runs on one GPU; multi-GPU runs are not part of this build "
+        print("bench.py: this sampler runs on one GPU; multi-GPU runs are not implemented "
               "(rows are independent: each GPU would run the same kernel on its share of the batch)",
               file=sys.stderr)
         sys.exit(2)

@@ -56,7 +56,7 @@ enum tc_status {
   TC_EHIP = 4,         /* a HIP runtime call failed */
   TC_ENOMEM = 5,       /* device allocation failed */
   TC_EDIST = 6,        /* nano: no token reached by the draw (nano:74) */
-  TC_EUNSUPPORTED = 7  /* this build does not implement the requested shape/option */
+  TC_EUNSUPPORTED = 7  /* this library does not implement the requested shape/option */
 };
 
 /* Sampler arithmetic to reproduce. */

@@ -1,6 +1,6 @@
 """ctypes wrapper over the C restatement in ``tc_oracle.c``.
 
-TEST INFRASTRUCTURE ONLY: this is the checker.  It may be imported by the test
+TEST INFRASTRUCTURE ONLY: this is the oracle.  It may be imported by the test
 suite, by the smoke check and by the CPU-baseline leg of the benchmark, never
 by the product package.
 """

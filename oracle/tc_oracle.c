@@ -1,7 +1,7 @@
 /*
  * tc_oracle.c -- CPU restatement of talechime's per-step token samplers.
  *
- * TEST INFRASTRUCTURE ONLY (the checker).  The product path never calls this.
+ * TEST INFRASTRUCTURE ONLY (the oracle).  The product path never calls this.
  *
  * Each function follows the Rust code cited next to it, keeping its element
  * types, its operation order and its summation order.  Where the reference

@@ -1,7 +1,7 @@
 /*
  * tc_oracle.h -- CPU restatement of talechime's five per-step token samplers.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker for the HIP sampler: only the
+ * TEST INFRASTRUCTURE ONLY.  This is the oracle for the HIP sampler: only the
  * test suite, the smoke check and the CPU-baseline leg of the benchmark may
  * load it.  The product library never links or calls it.
  *
