@@ -202,3 +202,23 @@ def test_qwen_large_vocab_bf16_bit_exact(sampler):
     n = np.minimum(g["keep_count"], CAP)
     for r in np.nonzero(ok)[0]:
         assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
+
+
+@pytest.mark.parametrize("name", list(synth.WORKLOADS))
+def test_device_matches_golden_fixture(sampler, name):
+    # the committed fixtures (tests/golden: the oracle's outputs on the first 8
+    # seeded rows of each workload) against the device, field for field
+    import os
+    w = synth.WORKLOADS[name]
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", f"{name}.npz"))
+    b = synth.make_batch(w, rows=8)
+    d = G.run_gpu(sampler, w, b, CAP)
+    amb = (g["flags"] & 1) != 0  # TC_FLAG_TIE_CUT: the reference leaves these ids open
+    assert np.array_equal(d["status"], g["status"])
+    assert np.array_equal(d["ids"][~amb], g["ids"][~amb])
+    assert np.array_equal(d["flags"] & ~16, g["flags"].astype(np.int32))
+    ok = ~amb
+    for k in ("topk_count", "keep_count"):
+        assert np.array_equal(d[k][ok], g[k][ok].astype(np.int32)), k
+    assert not [r for r in G.set_diff_rows(d, {k: g[k] for k in g.files}, CAP) if ok[r[0]]]
+    assert np.array_equal(d["norm"][ok].view(np.uint32), g["norm"][ok].view(np.uint32))
