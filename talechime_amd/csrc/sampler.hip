@@ -2391,9 +2391,7 @@ __device__ __forceinline__ bool cosy_fast(const RowArgs& a, CosyLds& U) {
     else cosy_fast_finish_t<2>(a, row, n, S, F);
   }
   __syncthreads();
-  const uint32_t top = F.out[0];
-  const bool ras = F.out[1] != 0u;
-  (void)top;
+  const bool ras = F.out[1] != 0u;  // the nucleus token (F.out[0]) is already written otherwise
   if (ras) {
     // random_sample_probs over every probability: exact terms for all (every
     // lane active: the wave-cooperative expf)
