@@ -1411,6 +1411,7 @@ constexpr int kLargeWords = kLargeVocab / 32;
 
 struct QLargeLds {
   uint32_t bits[kLargeWords];  // history ids and the EOS id
+  uint32_t psel[kLargeWords];  // history ids whose penalised logit reaches the candidate bound
   uint32_t hist[256];
   uint64_t cand[kLargeCand];   // rank order after the sort
   uint64_t candv[kLargeCand];  // vocabulary order
@@ -1492,6 +1493,7 @@ __device__ __forceinline__ LChunk decode_lchunk(const uint4 v, int q, int shift,
   return c;
 }
 
+__device__ __forceinline__ uint32_t pick_u32(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
 __device__ __forceinline__ uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
 
 // ckey(x) >> 16 for the f32 widening of a bf16 value b (both zeros give 0x8000)
@@ -1499,6 +1501,27 @@ __device__ __forceinline__ uint32_t bkey16(uint32_t b) {
   const uint32_t k = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
   return (b & 0x7fffu) ? k : 0x8000u;
 }
+
+// Two bf16 values per 32-bit word.  bkey16 of both halves: negative halves
+// complemented, positive ones with the top bit set, -0 raised to +0's key.
+__device__ __forceinline__ uint32_t bkey16x2(uint32_t w) {
+  const uint32_t sgn = w & 0x80008000u;
+  const uint32_t m = (sgn - (sgn >> 15)) | sgn;  // 0xffff in each negative half
+  const uint32_t k = w ^ (m | 0x80008000u);
+  const uint32_t nz = ((w & 0x7fff7fffu) + 0x7fff7fffu) & 0x80008000u;  // low 15 bits nonzero, per half
+  return k + ((sgn & ~nz) >> 15);
+}
+// 0x8000 in each half whose exponent bits are all ones (inf or NaN)
+__device__ __forceinline__ uint32_t nonfinite16x2(uint32_t w) {
+  const uint32_t e = (w & 0x7f807f80u) ^ 0x7f807f80u;
+  return ~((e + 0x7fff7fffu) & 0x80008000u) & 0x80008000u;
+}
+// 0xffff in the halves of word j whose bit (2j, 2j+1) of m8 is set
+__device__ __forceinline__ uint32_t half_mask(uint32_t m8, int j) {
+  const uint32_t t = (m8 >> (2 * j)) & 3u;
+  return __umul24((t & 1u) | ((t & 2u) << 15), 0xffffu);
+}
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 // The integer view of a chunk for the streaming passes: the bf16 bits of its 8
 // values, their keys, which are live (inside the row, not in the history, not
@@ -1594,8 +1617,11 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
   } else {
-    // the largest key outside the history, from the bf16 bits alone
+    // the largest key outside the history, from the bf16 bits alone, two
+    // values per instruction (v_pk_max_u16 over masked key pairs)
     uint4 raw[kLargeU], nxt[kLargeU];
+    u16x2 km2 = {0, 0};
+    uint32_t bad2 = 0;
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
     for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
@@ -1605,14 +1631,26 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       for (int u = 0; u < kLargeU; ++u) {
         const int q = q0 + u * bd;
         if (q >= nchunks) break;
-        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
-        bad |= c.bad ? 1u : 0u;
+        const int c0 = q * 8 - shift;  // in [-7, V)
+        const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
+        uint32_t inm = 0xffu;
+        if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+        if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+        const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+        const uint32_t live = inm & ~hb & ~em;
 #pragma unroll
-        for (int h = 0; h < 8; ++h) kmax = (((c.live >> h) & 1u) && c.k[h] > kmax) ? c.k[h] : kmax;
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t w = u4_word(raw[u], j);
+          const uint32_t k2 = bkey16x2(w) & half_mask(live, j);
+          km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(u16x2, k2));
+          bad2 |= nonfinite16x2(w) & half_mask(inm, j);
+        }
       }
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
+    kmax = km2.x > km2.y ? (uint32_t)km2.x : (uint32_t)km2.y;
+    bad = bad2 ? 1u : 0u;
   }
   bad = block_or_u(bad, S.s);
   if (bad) {  // NaN / inf: the reference's top-k takes its NaN path; not handled at this vocabulary
@@ -1684,62 +1722,86 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const uint32_t keyK = kmax - bK;
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
   const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
+  // the penalised ids whose logit reaches thr, from a sparse pass over the
+  // history (the EOS id's logit is -inf: never)
+  for (int w = t; w < nwords; w += bd) S.psel[w] = 0u;
+  __syncthreads();
+  if (a.do_pen) {
+    uint32_t h0, h1;
+    hist_range(a, row, &h0, &h1);
+    for (uint32_t k = h0 + (uint32_t)t; k < h1; k += (uint32_t)bd) {
+      const uint32_t id = a.hist_ids[k];
+      if (id < (uint32_t)V && (int)id != eos &&
+          logit(__uint_as_float((uint32_t)rp[id] << 16), true, (int)id) >= thr)
+        atomicOr(&S.psel[id >> 5], 1u << (id & 31u));
+    }
+  }
+  __syncthreads();
   // pass C: candidates in vocabulary order, a tile of kLargeU * blockDim
-  // chunks at a time, thread t holding the tile's chunks kLargeU * t + u
-  // The next tile's loads are issued before this tile's barrier.
+  // chunks at a time, thread t holding the tile's chunks kLargeU * t + u.
+  // Live ids are selected by key (two per instruction), penalised ones by
+  // the bitmap above.  The next tile's loads are issued before this tile's
+  // barrier.
   uint32_t n_c = 0;
   int parity = 0;
+  const u16x2 keyK2 = {(unsigned short)keyK, (unsigned short)keyK};
   uint4 raw[kLargeU], nxt[kLargeU];
 #pragma unroll
   for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(kLargeU * t + u, nchunks - 1)];
   for (int tb = 0; tb < nchunks; tb += kLargeU * bd, parity ^= 1) {
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + kLargeU * bd + kLargeU * t + u, nchunks - 1)];
-    // selected: live ids whose key reaches keyK, penalised ids whose logit
-    // reaches thr (the EOS id's logit is -inf: never); no branches per element
     uint64_t sel = 0, pens = 0;  // bit 8u + h
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
       const int q = tb + kLargeU * t + u;
       if (q < nchunks) {
-        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
+        const int c0 = q * 8 - shift;  // in [-7, V)
+        const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
+        const uint32_t ps = bits_at_fn(S.psel, nwords, c0) & 0xffu;
+        uint32_t inm = 0xffu;
+        if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+        if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+        const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+        const uint32_t live = inm & ~hb & ~em, pen = inm & hb & ~em;
+        uint32_t ge = 0;  // bit h: key >= keyK
 #pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const float x = __uint_as_float(c.b[h] << 16);
-          float vp = x * (x > 0.0f ? a.inv_pen : a.pen_f);
-          vp = a.do_temp ? vp * a.tmul + 0.0f : vp;
-          const bool ok = ((c.live >> h) & 1u) ? c.k[h] >= keyK : (((c.pen >> h) & 1u) != 0u && vp >= thr);
-          sel |= (ok ? 1ull : 0ull) << (8 * u + h);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
+          const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2), keyK2));
+          const uint32_t d = m2 ^ k2;  // 0 in a half where the key reaches keyK
+          const uint32_t nz = (((d & 0x7fff7fffu) + 0x7fff7fffu) | d) & 0x80008000u;
+          ge |= (((~nz >> 15) & 1u) | ((~nz >> 30) & 2u)) << (2 * j);
         }
-        pens |= (uint64_t)c.pen << (8 * u);
+        sel |= (uint64_t)((live & ge) | (pen & ps)) << (8 * u);
+        pens |= (uint64_t)pen << (8 * u);
       }
     }
     const uint32_t cnt = (uint32_t)__popcll(sel);
     const uint32_t ci = dpp_scan_u32(cnt);
     if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
     __syncthreads();
-    uint32_t off = n_c + ci - cnt, tile = 0;
-    for (int w = 0; w < num_waves(); ++w) {
-      const uint32_t tw = S.wtot[parity][w];
-      off += w < wave_id() ? tw : 0u;
-      tile += tw;
-    }
+    uint32_t off, tile;
+    wave_table_u32(S.wtot[parity], &off, &tile);
+    off += n_c + ci - cnt;
     if (sel && n_c + tile <= (uint32_t)kLargeCand) {
+      // the set bits only (a few per lane); the chunk index stays static so
+      // that the chunk registers are never indexed at run time
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
-        const int q = tb + kLargeU * t + u;
-#pragma unroll
-        for (int h = 0; h < 8; ++h)
-          if ((sel >> (8 * u + h)) & 1ull) {
-            const int e = q * 8 - shift + h;
-            const uint32_t wv = u4_word(raw[u], h >> 1);
-            const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
-            const float vv = logit(__uint_as_float(b), ((pens >> (8 * u + h)) & 1ull) != 0ull, e);
-            const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
-            S.cand[off] = kv;
-            S.candv[off] = kv;
-            ++off;
-          }
+        const uint32_t x = raw[u].x, y = raw[u].y, z = raw[u].z, w = raw[u].w;
+        const uint32_t pu = (uint32_t)(pens >> (8 * u));
+        for (uint32_t m = (uint32_t)(sel >> (8 * u)) & 0xffu; m; m &= m - 1u) {
+          const int h = __builtin_ctz(m);
+          const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
+          const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
+          const int e = (tb + kLargeU * t + u) * 8 - shift + h;
+          const float vv = logit(__uint_as_float(b), ((pu >> h) & 1u) != 0u, e);
+          const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
+          S.cand[off] = kv;
+          S.candv[off] = kv;
+          ++off;
+        }
       }
     }
     n_c += tile;
