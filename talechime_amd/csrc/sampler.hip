@@ -1405,13 +1405,13 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 constexpr int kLargeThreads = 1024;
 constexpr int kLargeCand = 2048;
 constexpr int kLargeU = 4;  // 16-byte chunks in flight per thread in the streaming passes
+constexpr int kLargeR = 2;  // tiles of kLargeU * blockDim chunks kept in registers across the passes
 constexpr int kLargePer = kLargeCand / kLargeThreads;  // candidate slots per thread
 constexpr int kLargeVocab = 262144;
 constexpr int kLargeWords = kLargeVocab / 32;
 
 struct QLargeLds {
   uint32_t bits[kLargeWords];  // history ids and the EOS id
-  uint32_t psel[kLargeWords];  // history ids whose penalised logit reaches the candidate bound
   uint32_t hist[256];
   uint64_t cand[kLargeCand];   // rank order after the sort
   uint64_t candv[kLargeCand];  // vocabulary order
@@ -1590,6 +1590,32 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   // Each streaming pass keeps kLargeU 16-byte loads in flight per thread (one
   // at a time leaves the pass bound by load latency, not by HBM).
   const int bd = (int)blockDim.x;
+  // The passes walk the row a tile of kLargeU * blockDim chunks at a time,
+  // thread t holding the tile's chunks kLargeU * t + u.  The first kLargeR
+  // tiles are loaded once (pass A) and stay in registers for passes B and C;
+  // the rest are streamed in every pass, the next tile's loads issued before
+  // the current tile's body.  The tile count depends on V only, so every
+  // thread runs every body (pass C's holds barriers).
+  const int tile = kLargeU * bd;
+  uint4 cache[kLargeR][kLargeU];
+  auto tiles = [&](auto&& body) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kLargeR; ++i)
+      if (i * tile < nchunks) body(cache[i], i * tile);
+    int tb = kLargeR * tile;
+    if (tb < nchunks) {
+      uint4 raw[kLargeU], nxt[kLargeU];
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(tb + kLargeU * t + u, nchunks - 1)];
+      for (; tb < nchunks; tb += tile) {
+#pragma unroll
+        for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
+        body(raw, tb);
+#pragma unroll
+        for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
+      }
+    }
+  };
   // pass A
   uint32_t bad = 0, kmax = 0;
   uint64_t best = 0;
@@ -1619,17 +1645,16 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   } else {
     // the largest key outside the history, from the bf16 bits alone, two
     // values per instruction (v_pk_max_u16 over masked key pairs)
-    uint4 raw[kLargeU], nxt[kLargeU];
     u16x2 km2 = {0, 0};
     uint32_t bad2 = 0;
 #pragma unroll
-    for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
-    for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
+    for (int i = 0; i < kLargeR; ++i)
 #pragma unroll
-      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(q0 + (kLargeU + u) * bd, nchunks - 1)];
+      for (int u = 0; u < kLargeU; ++u) cache[i][u] = base[min(i * tile + kLargeU * t + u, nchunks - 1)];
+    tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
-        const int q = q0 + u * bd;
+        const int q = tb + kLargeU * t + u;
         if (q >= nchunks) break;
         const int c0 = q * 8 - shift;  // in [-7, V)
         const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
@@ -1646,9 +1671,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
           bad2 |= nonfinite16x2(w) & half_mask(inm, j);
         }
       }
-#pragma unroll
-      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
-    }
+    });
     kmax = km2.x > km2.y ? (uint32_t)km2.x : (uint32_t)km2.y;
     bad = bad2 ? 1u : 0u;
   }
@@ -1676,28 +1699,19 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   }
   kmax = block_max_u(kmax, S.s);
   // pass B: exact histogram of the 256 keys at and below the largest
-  {
-    uint4 raw[kLargeU], nxt[kLargeU];
+  tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(t + u * bd, nchunks - 1)];
-    for (int q0 = t; q0 < nchunks; q0 += kLargeU * bd) {
+    for (int u = 0; u < kLargeU; ++u) {
+      const int q = tb + kLargeU * t + u;
+      if (q >= nchunks) break;
+      const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
 #pragma unroll
-      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(q0 + (kLargeU + u) * bd, nchunks - 1)];
-#pragma unroll
-      for (int u = 0; u < kLargeU; ++u) {
-        const int q = q0 + u * bd;
-        if (q >= nchunks) break;
-        const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const uint32_t dk = kmax - c.k[h];
-          if (((c.live >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
-        }
+      for (int h = 0; h < 8; ++h) {
+        const uint32_t dk = kmax - c.k[h];
+        if (((c.live >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
       }
-#pragma unroll
-      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
-  }
+  });
   __syncthreads();
   const uint32_t K = (uint32_t)a.K;
   if (wave_id() == 0) {
@@ -1722,35 +1736,34 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const uint32_t keyK = kmax - bK;
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
   const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
-  // the penalised ids whose logit reaches thr, from a sparse pass over the
-  // history (the EOS id's logit is -inf: never)
-  for (int w = t; w < nwords; w += bd) S.psel[w] = 0u;
-  __syncthreads();
+  // Penalised ids (in the history, not the EOS id) whose logit reaches thr.
+  // Their logit is a non-decreasing function of the bf16 value (a multiply by
+  // a positive factor, then by f32(1/T), each rounded), so they are the ids
+  // whose key reaches keyP, the smallest finite key whose penalised logit
+  // reaches thr (0xff80, above every finite key, when none does).  Both zeros
+  // share key 0x8000 and both give a logit of zero.  Every thread finds keyP
+  // by the same bisection over the finite keys [0x0080, 0xff7f].
+  uint32_t keyP = 0xff80u;
   if (a.do_pen) {
-    uint32_t h0, h1;
-    hist_range(a, row, &h0, &h1);
-    for (uint32_t k = h0 + (uint32_t)t; k < h1; k += (uint32_t)bd) {
-      const uint32_t id = a.hist_ids[k];
-      if (id < (uint32_t)V && (int)id != eos &&
-          logit(__uint_as_float((uint32_t)rp[id] << 16), true, (int)id) >= thr)
-        atomicOr(&S.psel[id >> 5], 1u << (id & 31u));
+    uint32_t lo = 0x0080u, hi = 0xff80u;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      const uint32_t b = (mid & 0x8000u) ? (mid & 0x7fffu) : (~mid & 0xffffu);
+      const float x = __uint_as_float(b << 16);
+      float v = x * (x > 0.0f ? a.inv_pen : a.pen_f);  // logit() for a penalised id that is not EOS
+      if (a.do_temp) v = v * a.tmul + 0.0f;
+      if (v >= thr) hi = mid;
+      else lo = mid + 1u;
     }
+    keyP = lo;
   }
-  __syncthreads();
-  // pass C: candidates in vocabulary order, a tile of kLargeU * blockDim
-  // chunks at a time, thread t holding the tile's chunks kLargeU * t + u.
-  // Live ids are selected by key (two per instruction), penalised ones by
-  // the bitmap above.  The next tile's loads are issued before this tile's
-  // barrier.
+  // pass C: candidates in vocabulary order, a tile at a time.  Live ids are
+  // selected by key (two per instruction), penalised ones by the bitmap
+  // above.
   uint32_t n_c = 0;
   int parity = 0;
-  const u16x2 keyK2 = {(unsigned short)keyK, (unsigned short)keyK};
-  uint4 raw[kLargeU], nxt[kLargeU];
-#pragma unroll
-  for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(kLargeU * t + u, nchunks - 1)];
-  for (int tb = 0; tb < nchunks; tb += kLargeU * bd, parity ^= 1) {
-#pragma unroll
-    for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + kLargeU * bd + kLargeU * t + u, nchunks - 1)];
+  const uint32_t kK32 = keyK * 0x00010001u, kP32 = keyP * 0x00010001u;  // the thresholds in both halves
+  tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
     uint64_t sel = 0, pens = 0;  // bit 8u + h
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
@@ -1758,22 +1771,23 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       if (q < nchunks) {
         const int c0 = q * 8 - shift;  // in [-7, V)
         const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-        const uint32_t ps = bits_at_fn(S.psel, nwords, c0) & 0xffu;
         uint32_t inm = 0xffu;
         if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
         if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
         const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
         const uint32_t live = inm & ~hb & ~em, pen = inm & hb & ~em;
-        uint32_t ge = 0;  // bit h: key >= keyK
+        uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
-          const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2), keyK2));
-          const uint32_t d = m2 ^ k2;  // 0 in a half where the key reaches keyK
+          const uint32_t th2 = kP32 ^ ((kK32 ^ kP32) & half_mask(live, j));
+          const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2),
+                                                                                     __builtin_bit_cast(u16x2, th2)));
+          const uint32_t d = m2 ^ k2;  // 0 in a half where the key reaches its threshold
           const uint32_t nz = (((d & 0x7fff7fffu) + 0x7fff7fffu) | d) & 0x80008000u;
           ge |= (((~nz >> 15) & 1u) | ((~nz >> 30) & 2u)) << (2 * j);
         }
-        sel |= (uint64_t)((live & ge) | (pen & ps)) << (8 * u);
+        sel |= (uint64_t)((live | pen) & ge) << (8 * u);
         pens |= (uint64_t)pen << (8 * u);
       }
     }
@@ -1781,10 +1795,10 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     const uint32_t ci = dpp_scan_u32(cnt);
     if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
     __syncthreads();
-    uint32_t off, tile;
-    wave_table_u32(S.wtot[parity], &off, &tile);
+    uint32_t off, ntile;
+    wave_table_u32(S.wtot[parity], &off, &ntile);
     off += n_c + ci - cnt;
-    if (sel && n_c + tile <= (uint32_t)kLargeCand) {
+    if (sel && n_c + ntile <= (uint32_t)kLargeCand) {
       // the set bits only (a few per lane); the chunk index stays static so
       // that the chunk registers are never indexed at run time
 #pragma unroll
@@ -1804,10 +1818,9 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
         }
       }
     }
-    n_c += tile;
-#pragma unroll
-    for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
-  }
+    n_c += ntile;
+    parity ^= 1;
+  });
   __syncthreads();
   if (n_c > (uint32_t)kLargeCand) {
     finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
