@@ -1411,6 +1411,7 @@ constexpr int kLargeVocab = 262144;
 constexpr int kLargeWords = kLargeVocab / 32;
 
 struct QLargeLds {
+  uint4 ltile[kLargeU * kLargeThreads];  // the row's tile kLargeR (chunk kLargeU * t + u at u * blockDim + t)
   uint32_t bits[kLargeWords];  // history ids and the EOS id
   uint32_t hist[256];
   uint64_t cand[kLargeCand];   // rank order after the sort
@@ -1593,27 +1594,38 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   // The passes walk the row a tile of kLargeU * blockDim chunks at a time,
   // thread t holding the tile's chunks kLargeU * t + u.  The first kLargeR
   // tiles are loaded once (pass A) and stay in registers for passes B and C;
-  // the rest are streamed in every pass, the next tile's loads issued before
-  // the current tile's body.  The tile count depends on V only, so every
-  // thread runs every body (pass C's holds barriers).
+  // tile kLargeR is loaded once and kept in LDS, each thread reading back only
+  // the slots it wrote; the rest are streamed in every pass, the next tile's
+  // loads issued before the current tile's body.  The tile count depends on V
+  // only, so every thread runs every body (pass C's holds barriers).
   const int tile = kLargeU * bd;
   uint4 cache[kLargeR][kLargeU];
-  auto tiles = [&](auto&& body) __attribute__((always_inline)) {
+  auto tiles = [&](bool fill, auto&& body) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kLargeR; ++i)
       if (i * tile < nchunks) body(cache[i], i * tile);
     int tb = kLargeR * tile;
+    uint4 raw[kLargeU], nxt[kLargeU];
     if (tb < nchunks) {
-      uint4 raw[kLargeU], nxt[kLargeU];
 #pragma unroll
-      for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(tb + kLargeU * t + u, nchunks - 1)];
-      for (; tb < nchunks; tb += tile) {
+      for (int u = 0; u < kLargeU; ++u) raw[u] = fill ? base[min(tb + kLargeU * t + u, nchunks - 1)] : S.ltile[u * bd + t];
 #pragma unroll
-        for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
-        body(raw, tb);
+      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
+      if (fill) {
 #pragma unroll
-        for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
+        for (int u = 0; u < kLargeU; ++u) S.ltile[u * bd + t] = raw[u];
       }
+      body(raw, tb);
+      tb += tile;
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
+    }
+    for (; tb < nchunks; tb += tile) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
+      body(raw, tb);
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
   };
   // pass A
@@ -1651,7 +1663,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     for (int i = 0; i < kLargeR; ++i)
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) cache[i][u] = base[min(i * tile + kLargeU * t + u, nchunks - 1)];
-    tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+    tiles(true, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
@@ -1699,7 +1711,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   }
   kmax = block_max_u(kmax, S.s);
   // pass B: exact histogram of the 256 keys at and below the largest
-  tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+  tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
       const int q = tb + kLargeU * t + u;
@@ -1763,7 +1775,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   uint32_t n_c = 0;
   int parity = 0;
   const uint32_t kK32 = keyK * 0x00010001u, kP32 = keyP * 0x00010001u;  // the thresholds in both halves
-  tiles([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+  tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
     uint64_t sel = 0, pens = 0;  // bit 8u + h
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
