@@ -1497,14 +1497,9 @@ __device__ __forceinline__ LChunk decode_lchunk(const uint4 v, int q, int shift,
 __device__ __forceinline__ uint32_t pick_u32(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
 __device__ __forceinline__ uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
 
-// ckey(x) >> 16 for the f32 widening of a bf16 value b (both zeros give 0x8000)
-__device__ __forceinline__ uint32_t bkey16(uint32_t b) {
-  const uint32_t k = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
-  return (b & 0x7fffu) ? k : 0x8000u;
-}
-
-// Two bf16 values per 32-bit word.  bkey16 of both halves: negative halves
-// complemented, positive ones with the top bit set, -0 raised to +0's key.
+// ckey(x) >> 16 for the f32 widening of the two bf16 values of a 32-bit word:
+// negative halves complemented, positive ones with the top bit set, -0
+// raised to +0's key (both zeros give 0x8000).
 __device__ __forceinline__ uint32_t bkey16x2(uint32_t w) {
   const uint32_t sgn = w & 0x80008000u;
   const uint32_t m = (sgn - (sgn >> 15)) | sgn;  // 0xffff in each negative half
@@ -1523,39 +1518,6 @@ __device__ __forceinline__ uint32_t half_mask(uint32_t m8, int j) {
   return __umul24((t & 1u) | ((t & 2u) << 15), 0xffffu);
 }
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-
-// The integer view of a chunk for the streaming passes: the bf16 bits of its 8
-// values, their keys, which are live (inside the row, not in the history, not
-// the EOS id), which are penalised (inside the row, in the history, not the
-// EOS id), and whether a value inside the row is non-finite.
-struct KChunk {
-  uint32_t b[8];
-  uint32_t k[8];
-  uint32_t live, pen;
-  bool bad;
-};
-__device__ __forceinline__ KChunk key_chunk(const uint4 v, int q, int shift, int V, const uint32_t* bits, int nwords,
-                                            int eos) {
-  KChunk c;
-  const int e0 = q * 8 - shift;  // in [-7, V): q < nchunks
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  const uint32_t hb = bits_at_fn(bits, nwords, e0) & 0xffu;
-  uint32_t inm = 0xffu;
-  if (e0 < 0) inm &= 0xffu << (uint32_t)(-e0);
-  if (e0 + 8 > V) inm &= (1u << (uint32_t)(V - e0)) - 1u;
-  const uint32_t em = (eos >= e0 && eos < e0 + 8) ? 1u << (uint32_t)(eos - e0) : 0u;
-  c.live = inm & ~hb & ~em;
-  c.pen = inm & hb & ~em;
-  c.bad = false;
-#pragma unroll
-  for (int h = 0; h < 8; ++h) {
-    const uint32_t b = (h & 1) ? (w[h >> 1] >> 16) : (w[h >> 1] & 0xffffu);
-    c.b[h] = b;
-    c.bad |= ((inm >> h) & 1u) && (b & 0x7f80u) == 0x7f80u;
-    c.k[h] = bkey16(b);
-  }
-  return c;
-}
 
 __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   __shared__ QLargeLds S;
@@ -1711,16 +1673,26 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   }
   kmax = block_max_u(kmax, S.s);
   // pass B: exact histogram of the 256 keys at and below the largest
+  // (two keys per 32-bit operation; a live key is at most kmax, so its
+  // 16-bit distance below kmax does not wrap)
+  const u16x2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
   tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
       const int q = tb + kLargeU * t + u;
       if (q >= nchunks) break;
-      const KChunk c = key_chunk(raw[u], q, shift, V, S.bits, nwords, eos);
+      const int c0 = q * 8 - shift;  // in [-7, V)
+      const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
+      uint32_t inm = 0xffu;
+      if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+      if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+      const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+      const uint32_t live = inm & ~hb & ~em;
 #pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const uint32_t dk = kmax - c.k[h];
-        if (((c.live >> h) & 1u) && dk < 256u) atomicAdd(&S.hist[dk], 1u);
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, bkey16x2(u4_word(raw[u], j))));
+        if (((live >> (2 * j)) & 1u) && (d2 & 0xff00u) == 0u) atomicAdd(&S.hist[d2 & 0xffu], 1u);
+        if (((live >> (2 * j + 1)) & 1u) && (d2 >> 24) == 0u) atomicAdd(&S.hist[(d2 >> 16) & 0xffu], 1u);
       }
     }
   });
