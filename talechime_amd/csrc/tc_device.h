@@ -428,22 +428,38 @@ __device__ __forceinline__ bool block_kth_largest(const uint32_t (&key)[ITEMS], 
   return true;
 }
 
-// In-place ascending bitonic sort of n_pad (a power of two) 64-bit keys in LDS.
+// In-place ascending bitonic sort of n_pad (a power of two) 64-bit keys in LDS
+// by the whole block.  Each stage (k, j) gives thread p the pairs
+// p + r * blockDim, pair p ordering elements i = 2 (p & ~(j-1)) + (p & (j-1)) and i + j.  While j <= 64
+// the pairs 64w .. 64w+63 touch only elements 128w .. 128w+127, so with
+// blockDim a multiple of 64 each such segment belongs to one wave.  Between
+// two stages that both stay inside segments the wave orders its own LDS
+// accesses (one wave's LDS operations complete in order; the fences keep the
+// compiler from moving them); any other boundary takes a block barrier.
 __device__ __forceinline__ void block_bitonic_sort(uint64_t* a, int n_pad) {
+  const int half = n_pad >> 1;
+  const bool segs = (blockDim.x & 63u) == 0u;
   for (int k = 2; k <= n_pad; k <<= 1) {
     for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < n_pad; i += blockDim.x) {
-        int ixj = i ^ j;
-        if (ixj > i) {
-          uint64_t x = a[i], y = a[ixj];
-          bool up = (i & k) == 0;
-          if ((x > y) == up) {
-            a[i] = y;
-            a[ixj] = x;
-          }
+      for (int p = threadIdx.x; p < half; p += blockDim.x) {
+        const int i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+        const int ixj = i + j;
+        const uint64_t x = a[i], y = a[ixj];
+        const bool up = (i & k) == 0;
+        if ((x > y) == up) {
+          a[i] = y;
+          a[ixj] = x;
         }
       }
-      __syncthreads();
+      // the next stage is (k, j/2), or (2k, k) after j == 1
+      const bool next_in_seg = j > 1 ? true : (2 * k <= n_pad && k <= 64);
+      if (segs && j <= 64 && next_in_seg) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else {
+        __syncthreads();
+      }
     }
   }
 }
