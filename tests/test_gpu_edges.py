@@ -630,6 +630,26 @@ def test_qwen_large_vocab_shapes(sampler, V):
         same(g, o, rows=[r for r in range(rows) if not tie[r]])
 
 
+@pytest.mark.parametrize("top_k", [1, 2, 3, 7, 64, 100, 300, 513])
+def test_qwen_large_vocab_candidate_counts(sampler, top_k):
+    # candidate lists from 1 to about 600 ids: the rank sort runs at every
+    # power-of-two size from 2 to 1024 keys (its wave-local and block-wide
+    # stages), with and without penalised ids among the candidates
+    V = 151936
+    g_ = np.random.default_rng(1000 + top_k)
+    rows = 4
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    top = np.argsort(-x, axis=1)[:, :top_k + 8]
+    hist = [top[r, ::3].tolist() + g_.integers(0, V, 200).tolist() for r in range(rows)]
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.7, top_p=0.95, penalty=1.1), dict(temperature=1.0, top_p=0.5, penalty=0.8),
+               dict(temperature=0.9, top_p=1.0, penalty=1.0)):
+        g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, top_k=top_k, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
 def test_qwen_large_vocab_greedy_broadcast_and_unsupported(sampler):
     g_ = np.random.default_rng(5)
     V = 151936
