@@ -1405,7 +1405,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 constexpr int kLargeThreads = 1024;
 constexpr int kLargeCand = 2048;
 constexpr int kLargeU = 4;  // 16-byte chunks in flight per thread in the streaming passes
-constexpr int kLargeR = 2;  // tiles of kLargeU * blockDim chunks kept in registers across the passes
+constexpr int kLargeR = 3;  // tiles of kLargeU * blockDim chunks kept in registers across the passes
 constexpr int kLargePer = kLargeCand / kLargeThreads;  // candidate slots per thread
 constexpr int kLargeVocab = 262144;
 constexpr int kLargeWords = kLargeVocab / 32;
