@@ -8,15 +8,19 @@ top-p 0.8, one f64 uniform per row), with inputs already resident in HBM.
 Batches rotate through a pool larger than twice the 256 MB Infinity Cache so
 every step streams its logits from HBM.
 
-The timed region replays a HIP graph holding one launch per pool batch, so
-the launches run back to back on the GPU (a launch from Python costs a few
-tens of microseconds of host time; that host-inclusive rate is reported under
-"timing").  Prints one JSON line: rows/s for the whole job, the roofline
-figure of the sampler kernel (algorithmic bytes per launch over its average
-duration, timed with HIP events on the launch stream), and the CPU baseline
-(the oracle timed on this host on a bounded sample of the same workload).
+The timed region is exactly --steps launches, captured in HIP graphs (one
+launch per pool batch) and replayed, so the launches run back to back on the
+GPU (a launch from Python costs a few tens of microseconds of host time; that
+host-inclusive rate is reported under "timing").  Prints one JSON line:
+rows/s for the whole job, the roofline figure of the sampler kernel
+(algorithmic bytes per launch over its average duration, timed with HIP
+events on the launch stream), "parity" (the device's ids on pool batches
+against the oracle's, with the tie and unsupported rows counted) and the CPU
+baseline (the oracle timed on this host, one thread and row-parallel, on a
+bounded sample of the same workload).
 
     python bench.py [--gpus 1] [--steps 2000] [--warmup 200]
+    python bench.py --parity 4      # boundary-row counts of every workload
 """
 from __future__ import annotations
 
@@ -41,6 +45,11 @@ def parse():
     ap.add_argument("--pool-mb", type=int, default=640, help="rotating input pool (MB of logits)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--parity-batches", type=int, default=8,
+                    help="pool batches whose ids are compared with the oracle after the timed region")
+    ap.add_argument("--parity", type=int, default=0, metavar="N",
+                    help="instead of timing: compare N seeded batches of every workload with the oracle "
+                         "and print the boundary-row counts")
     ap.add_argument("--beam", type=int, default=0, metavar="B",
                     help="time the indextts beam-sample step over B elements x 3 beams instead")
     ap.add_argument("--copy-calib", action="store_true",
@@ -64,22 +73,130 @@ def measured_traffic(workload: str):
     return None
 
 
+def host_cpus():
+    """(threads to use, CPUs this process may run on, nproc, CPU model)."""
+    nproc = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        avail = nproc
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:  # pragma: no cover
+        pass
+    # one GPU's share of a shared host is 16 CPUs, whatever nproc reports
+    return max(1, min(avail, 16)), avail, nproc, model
+
+
+def _oracle_rate(O, p, w, batch, seconds: float, nthreads: int):
+    rows = batch.logits_f32.shape[0]
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.sample(p, batch.logits_f32, batch.hist_off, batch.hist_ids, batch.uniforms, nthreads=nthreads)
+        done += rows
+    return done, time.perf_counter() - t0
+
+
 def cpu_baseline(w, batch, seconds: float):
-    """The oracle (C restatement of the reference Rust sampler) on this host."""
+    """The oracle (C restatement of the reference Rust sampler) on this host:
+    one thread (the reference loops over rows serially) and row-parallel over
+    the host's CPUs (OpenMP over rows)."""
     from oracle import oracle as O
 
     p = O.make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p,
                       penalty=w.penalty, min_keep=w.min_keep, ras_win=w.ras_win, ras_tau=w.ras_tau)
     rows = batch.logits_f32.shape[0]
     O.sample(p, batch.logits_f32[:8], batch.hist_off[:9], batch.hist_ids, batch.uniforms[:8 * w.n_uniforms])
-    done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        O.sample(p, batch.logits_f32, batch.hist_off, batch.hist_ids, batch.uniforms, nthreads=1)
-        done += rows
-    dt = time.perf_counter() - t0
-    return {"value": round(done / dt, 1), "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{done} rows of {w.name} ({done // rows} passes over one seeded batch), "
-                      f"single thread, {dt:.1f} s"}
+    threads, avail, nproc, model = host_cpus()
+    d1, t1 = _oracle_rate(O, p, w, batch, seconds, 1)
+    dn, tn = _oracle_rate(O, p, w, batch, seconds / 2, threads)
+    return {"value": round(dn / tn, 1), "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{dn} rows of {w.name} ({dn // rows} passes over one seeded batch), rows split over "
+                      f"{threads} threads, {tn:.1f} s",
+            "single_thread": {"value": round(d1 / t1, 1), "unit": "rows/s", "cores": 1,
+                              "sample": f"{d1} rows ({d1 // rows} passes), one thread, {t1:.1f} s"},
+            "host": {"nproc": nproc, "affinity_cpus": avail, "cpu_model": model}}
+
+
+def parity_counts(ids, st, fl, o):
+    """Device outputs (production path, no verification outputs) against the
+    oracle's on the same rows: the boundary rows are counted, not hidden."""
+    ok = (st == 0) & (o["status"] == 0)
+    tie = ((fl & 1) != 0) | ((o["flags"] & 1) != 0)
+    near = (fl & 16) != 0
+    diff = ok & (ids != o["ids"])
+    return {"rows": int(ids.size), "both_ok": int(ok.sum()), "ids_equal": int((ok & (ids == o["ids"])).sum()),
+            "status_mismatch": int((st != o["status"]).sum()), "unsupported": int((st == 7).sum()),
+            "tie_cut_rows": int(tie.sum()), "near_tie_rows": int(near.sum()),
+            "ids_differ_on_tie_rows": int((diff & (tie | near)).sum()),
+            "ids_differ_elsewhere": int((diff & ~(tie | near)).sum())}
+
+
+def merge_counts(acc, c):
+    if acc is None:
+        return dict(c)
+    return {k: acc[k] + c[k] for k in acc}
+
+
+def pool_parity(w, logits, hists, hoff, unis, sampler, params, n_batches):
+    """Pool batches sampled on the device compared with the oracle on the host."""
+    import torch
+
+    from oracle import oracle as O
+
+    p = O.make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p,
+                      penalty=w.penalty, min_keep=w.min_keep, ras_win=w.ras_win, ras_tau=w.ras_tau)
+    threads = host_cpus()[0]
+    acc = None
+    ho = hoff.cpu().numpy().view(np.uint32)
+    for j in range(min(n_batches, len(logits))):
+        r = sampler.sample(params, logits[j], hoff, hists[j], unis[j])
+        torch.cuda.synchronize()
+        x = logits[j].float().cpu().numpy()
+        o = O.sample(p, x, ho, hists[j].cpu().numpy().view(np.uint32), unis[j].cpu().numpy(), nthreads=threads)
+        acc = merge_counts(acc, parity_counts(r.ids.cpu().numpy().view(np.uint32), r.status.cpu().numpy(),
+                                              r.flags.cpu().numpy().view(np.uint32), o))
+    acc["batches"] = min(n_batches, len(logits))
+    return acc
+
+
+def parity_all(n_batches: int):
+    """Every workload: n seeded batches on the device against the oracle."""
+    import torch
+
+    from oracle import oracle as O
+    from talechime_amd import synth
+    from talechime_amd.sampler import DeviceSampler, make_params
+
+    dev = torch.device("cuda", 0)
+    threads = host_cpus()[0]
+    for name, w in synth.WORKLOADS.items():
+        sampler = DeviceSampler(0, max_rows=w.rows, max_vocab=w.vocab)
+        kw = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
+                  min_keep=w.min_keep, ras_win=w.ras_win, ras_tau=w.ras_tau)
+        params, op = make_params(w.variant, **kw), O.make_params(w.variant, **kw)
+        acc = None
+        for bi in range(n_batches):
+            b = synth.make_batch(w, batch_index=bi)
+            if w.dtype == "bf16":
+                lg = torch.from_numpy(b.logits.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+            else:
+                lg = torch.from_numpy(b.logits).to(dev)
+            hid = b.hist_ids if b.hist_ids.size else np.zeros(1, np.uint32)
+            r = sampler.sample(params, lg, torch.from_numpy(b.hist_off.view(np.int32).copy()).to(dev),
+                               torch.from_numpy(hid.view(np.int32).copy()).to(dev),
+                               torch.from_numpy(b.uniforms).to(dev))
+            torch.cuda.synchronize()
+            o = O.sample(op, b.logits_f32, b.hist_off, b.hist_ids, b.uniforms, nthreads=threads)
+            acc = merge_counts(acc, parity_counts(r.ids.cpu().numpy().view(np.uint32), r.status.cpu().numpy(),
+                                                  r.flags.cpu().numpy().view(np.uint32), o))
+        sampler.close()
+        acc["batches"] = n_batches
+        print(json.dumps({"workload": name, **acc}), flush=True)
 
 
 def beam_bench(args):
@@ -119,20 +236,30 @@ def beam_bench(args):
         step(i % n_pool)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for j in range(n_pool):
-            step(j)
-    graph.replay()
+
+    def capture(n):
+        if n == 0:
+            return None
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for j in range(n):
+                step(j)
+        return gr
+
+    K = max(1, args.steps)
+    full_replays, rest = divmod(K, n_pool)
+    full, part = capture(n_pool), capture(rest)
+    full.replay()
     torch.cuda.synchronize()
-    replays = max(1, -(-args.steps // n_pool))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(replays):
-        graph.replay()
+    for _ in range(full_replays):
+        full.replay()
+    if part is not None:
+        part.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    steps = replays * n_pool
+    steps = full_replays * n_pool + rest
     ms = e0.elapsed_time(e1) / steps
     st = outs[0].status.cpu().numpy()
     if (st != 0).any():
@@ -157,7 +284,8 @@ def beam_bench(args):
         "dtype": "f32", "data": "synthetic (seeded mel-code rows, running beam scores; rotating pool)",
         "config": {"workload": f"indextts-beam-{B}x{nb}x{w.vocab}", "elements": B, "num_beams": nb,
                    "n_draws": 2 * nb, "pool_batches": n_pool},
-        "timing": f"{replays} replays of a HIP graph of {n_pool} steps (row pass + joint draws each)",
+        "timing": f"{steps} steps (row pass + joint draws each): {full_replays} replays of a HIP graph of "
+                  f"{n_pool} steps" + (f" and one of {rest}" if rest else ""),
         **extra,
     }), flush=True)
 
@@ -189,6 +317,8 @@ def main():
         sys.exit(2)
     if args.beam:
         return beam_bench(args)
+    if args.parity:
+        return parity_all(args.parity)
     import torch
 
     from talechime_amd import synth
@@ -246,30 +376,44 @@ def main():
     e1.record(stream)
     torch.cuda.synchronize()
     eager_us = e0.elapsed_time(e1) * 1e3 / n_e
-    # the timed region: one launch per pool batch captured in a HIP graph and
-    # replayed, so the launches run back to back on the GPU
-    n_graph = min(n_pool, 256)
-    graph = torch.cuda.CUDAGraph()
-    side = torch.cuda.Stream(device=dev)
-    side.wait_stream(stream)
-    with torch.cuda.stream(side):
-        for j in range(n_graph):
-            step(j)
-    stream.wait_stream(side)
-    torch.cuda.synchronize()
-    with torch.cuda.graph(graph):
-        for j in range(n_graph):
-            step(j)
-    replays = max(1, -(-args.steps // n_graph))
-    graph.replay()
+    # the timed region: exactly `steps` launches, batch i % n_pool for launch i,
+    # captured in HIP graphs (one of the whole pool, one of the remainder) and
+    # replayed, so the launches run back to back on the GPU.  The untimed replay
+    # of the whole pool before it ends on the last batch, so the first timed
+    # batches were last read n_pool - 1 launches (more than the Infinity Cache)
+    # earlier.
+    K = max(1, args.steps)
+
+    def capture(n):
+        if n == 0:
+            return None
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for j in range(n):
+                step(j)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for j in range(n):
+                step(j)
+        return gr
+
+    full = capture(n_pool)
+    full_replays, rest = divmod(K, n_pool)
+    part = capture(rest)
+    full.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(replays):
-        graph.replay()
+    for _ in range(full_replays):
+        full.replay()
+    if part is not None:
+        part.replay()
     e1.record(stream)
     torch.cuda.synchronize()
-    steps_done = replays * n_graph
+    steps_done = full_replays * n_pool + rest
     ms_per_step = e0.elapsed_time(e1) / steps_done
     k_avg_us = ms_per_step * 1e3
     # every row of the seeded batch sampled cleanly, and the graph's ids equal the eager launch's
@@ -308,9 +452,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(w.name),
                      "kernel_avg_us": round(k_avg_us, 3), "algorithmic_bytes_per_launch": bytes_per_launch},
-        "timing": f"{replays} replays of a HIP graph of {n_graph} launches (one per pool batch); "
-                  f"launched one by one from Python: {eager_us:.1f} us per step",
+        "timing": f"{steps_done} launches: {full_replays} replays of a HIP graph of the {n_pool}-batch pool"
+                  + (f" and one of {rest} launches" if rest else "")
+                  + f"; launched one by one from Python: {eager_us:.1f} us per step",
     }
+    res["parity"] = pool_parity(w, logits, hists, hoff, unis, sampler, params, args.parity_batches)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(w, batch, args.cpu_seconds)
     sampler.close()

@@ -38,10 +38,6 @@ class Params(C.Structure):
         ("typical_mass", C.c_double),
         ("add_mask", C.c_void_p),
         ("pen_mask", C.c_void_p),
-        ("dev_items", C.c_int32),
-        ("dev_threads", C.c_int32),
-        ("dev_align", C.c_int32),
-        ("dev_ld", C.c_int64),
     ]
 
 
@@ -331,17 +327,13 @@ def cosy_random(probs, u1):
 # ---------------------------------------------------------------- batch pipeline
 def make_params(variant, *, temperature=1.0, top_p=1.0, penalty=1.0, top_k=0, min_keep=2,
                 ras_win=10, ras_tau=0.1, eos_id=-1, exclude_id=-1, typical=False,
-                typical_mass=0.9, hist_mode=HIST_PER_ROW, add_mask=None, pen_mask=None,
-                dev_order=None):
-    """dev_order = (items, threads, align, ld) selects the device summation order."""
+                typical_mass=0.9, hist_mode=HIST_PER_ROW, add_mask=None, pen_mask=None):
     p = Params()
     p.variant, p.hist_mode = variant, hist_mode
     p.temperature, p.top_p, p.penalty = temperature, top_p, penalty
     p.top_k, p.min_keep, p.ras_win, p.ras_tau = top_k, min_keep, ras_win, ras_tau
     p.eos_id, p.exclude_id = eos_id, exclude_id
     p.typical, p.typical_mass = int(typical), typical_mass
-    if dev_order is not None:
-        p.dev_items, p.dev_threads, p.dev_align, p.dev_ld = dev_order
     keep = []
     if add_mask is not None:
         a = np.ascontiguousarray(add_mask, np.float32)

@@ -58,33 +58,6 @@ static inline uint64_t tkey64(double d) {
 static inline float rmaxf(float a, float b) { return isnan(a) ? b : (isnan(b) ? a : (a > b ? a : b)); }
 static inline double rmax(double a, double b) { return isnan(a) ? b : (isnan(b) ? a : (a > b ? a : b)); }
 
-/* Sum of v[0..V) in the device's reduction order (see tco_params.dev_*). */
-static float dev_order_sum(const float* v, size_t V, size_t row, const tco_params* p) {
-  int items = p->dev_items, threads = p->dev_threads;
-  long long shift = (long long)(((long long)row * p->dev_ld) % p->dev_align);
-  int waves = threads / 64;
-  float total = 0.0f;
-  for (int w = 0; w < waves; w++) {
-    float lane[64];
-    for (int l = 0; l < 64; l++) {
-      long long t = (long long)w * 64 + l;
-      float part = 0.0f;
-      for (int i = 0; i < items; i++) {
-        long long e = t * items + i - shift;
-        if (e >= 0 && e < (long long)V) part += v[e];
-      }
-      lane[l] = part;
-    }
-    for (int o = 32; o > 0; o >>= 1) {
-      float nxt[64];
-      for (int l = 0; l < 64; l++) nxt[l] = lane[l] + lane[l ^ o];
-      memcpy(lane, nxt, sizeof lane);
-    }
-    total = (w == 0) ? lane[0] : total + lane[0];
-  }
-  return total;
-}
-
 static int cmp_u64(const void* a, const void* b) {
   uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
   return (x > y) - (x < y);
@@ -656,14 +629,7 @@ static int row_cosy(const tco_params* p, float* x, size_t V, size_t row, const u
   if (p->eos_id >= 0) {
     for (size_t i = 0; i < V; i++) x[i] = x[i] + ((size_t)p->eos_id == i ? -INFINITY : 0.0f);
   }
-  if (p->dev_threads > 0) {
-    float max = -INFINITY;
-    for (size_t i = 0; i < V; i++) max = rmaxf(max, x[i]);
-    for (size_t i = 0; i < V; i++) x[i] = expf(x[i] - max);
-    float sum = dev_order_sum(x, V, row, p);
-    for (size_t i = 0; i < V; i++) x[i] /= sum;
-    if (rv) rv->norm = sum;
-  } else {
+  {
     float sum = softmax_last_dim_sum(x, V);
     if (rv) rv->norm = sum;
   }

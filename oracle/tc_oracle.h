@@ -70,17 +70,6 @@ typedef struct tco_params {
   double typical_mass;
   const float* add_mask;   /* qwen additive suppression mask [V] or NULL */
   const float* pen_mask;   /* qwen penalty mask [V] (hist_mode == MASK) */
-  /* Device summation order for the full-row sums (indextts log_softmax, cosyvoice3
-   * softmax).  dev_threads == 0: the reference's sequential order.  Otherwise the
-   * sum is taken as the device does: thread t sums its dev_items consecutive
-   * elements e = t*dev_items + i - shift (shift = (row * dev_ld) % dev_align), each
-   * 64-thread wave combines by a butterfly (v += v[lane ^ o], o = 32..1), and the
-   * wave sums are added in wave order.  indextts then uses the correctly rounded
-   * expf/logf, as the device does for that sum. */
-  int32_t dev_items;
-  int32_t dev_threads;
-  int32_t dev_align;
-  int64_t dev_ld;
 } tco_params;
 
 /* Per-row verification outputs (any pointer may be NULL). */

@@ -5,7 +5,7 @@ import torch
 
 from oracle import oracle as O
 from talechime_amd import synth
-from talechime_amd.sampler import DeviceSampler, launch_shape, make_params
+from talechime_amd.sampler import DeviceSampler, make_params
 
 ORACLE_THREADS = 8
 
@@ -21,19 +21,13 @@ def to_dev(b: synth.Batch, w: synth.Workload, dev="cuda"):
     return logits, ho, hi, un
 
 
-def params_for(w: synth.Workload, lib: str, dev_order=None, **over):
+def params_for(w: synth.Workload, lib: str, **over):
     kw = dict(temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
               min_keep=w.min_keep, ras_win=w.ras_win, ras_tau=w.ras_tau)
     kw.update(over)
     if lib == "oracle":
-        return O.make_params(w.variant, dev_order=dev_order, **kw)
+        return O.make_params(w.variant, **kw)
     return make_params(w.variant, **kw)
-
-
-def dev_order_for(w: synth.Workload, ld: int):
-    dt = 1 if w.dtype == "bf16" else 0
-    items, threads = launch_shape(w.vocab, dt)
-    return (items, threads, 8 if dt else 4, ld)
 
 
 def run_gpu(sampler: DeviceSampler, w, b, cap=64, **over):
@@ -47,8 +41,8 @@ def run_gpu(sampler: DeviceSampler, w, b, cap=64, **over):
     return out
 
 
-def run_oracle(w, b, cap=64, dev_order=None, **over):
-    p = params_for(w, "oracle", dev_order=dev_order, **over)
+def run_oracle(w, b, cap=64, **over):
+    p = params_for(w, "oracle", **over)
     return O.sample(p, b.logits_f32, b.hist_off, b.hist_ids, b.uniforms, cap=cap, nthreads=ORACLE_THREADS)
 
 

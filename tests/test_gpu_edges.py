@@ -9,7 +9,7 @@ torch = pytest.importorskip("torch")
 
 from oracle import oracle as O  # noqa: E402
 from talechime_amd import _lib  # noqa: E402
-from talechime_amd.sampler import DeviceSampler, launch_shape, make_params  # noqa: E402
+from talechime_amd.sampler import DeviceSampler, make_params  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 NEG = -np.inf
@@ -26,7 +26,7 @@ def sampler():
     s.close()
 
 
-def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=False, dev_order=False,
+def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=False,
         hist_mode=0, add_mask=None, pen_mask=None, **kw):
     """Sample with both the GPU and the oracle; returns (gpu dict, oracle dict)."""
     x = np.ascontiguousarray(logits, np.float32)
@@ -79,14 +79,9 @@ def run(sampler, variant, logits, hist=None, uniforms=None, *, ld_pad=0, bf16=Fa
         assert np.array_equal(ids0[keep], g["ids"][keep]), np.nonzero(ids0 != g["ids"])[0][:10]
         if variant == O.QWEN:
             assert np.array_equal(r0.flags.cpu().numpy(), g["flags"])
-    dord = None
-    if dev_order and variant == O.COSY_RAS:
-        items, threads = launch_shape(V, 1 if bf16 else 0)
-        dord = (items, threads, 8 if bf16 else 4, ld)
     okw = dict(kw)
     okw["penalty"] = okw.pop("penalty", 1.0)
-    op = O.make_params(variant, hist_mode=hist_mode, add_mask=add_mask, pen_mask=pen_mask,
-                       dev_order=dord, **okw)
+    op = O.make_params(variant, hist_mode=hist_mode, add_mask=add_mask, pen_mask=pen_mask, **okw)
     o = O.sample(op, x, off, ids, u, cap=CAP)
     return g, o
 
