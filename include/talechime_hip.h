@@ -185,6 +185,26 @@ int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* params, const voi
                           uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
                           uint32_t* d_out_flags, tc_stream stream);
 
+/*
+ * tc_indextts_beam_step without any allocation.  No counterpart in the reference:
+ * this entry point is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and row-level statuses as tc_indextts_beam_step, on the
+ * current device and without a context.  The row-pass workspace is a file-scope
+ * device array sized for batch * num_beams <= TC_NOALLOC_BEAM_ROWS (4.2 MB per GPU,
+ * held until the process ends); larger calls return TC_EINVAL, vocabularies above
+ * 16384 TC_EUNSUPPORTED.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (different streams, or threads without ordering) race.  The
+ * first call on a device (or tc_create on it) resolves the array's address.
+ */
+#define TC_NOALLOC_BEAM_ROWS 256
+int tc_indextts_beam_step_noalloc(const tc_sample_params* params, const void* d_logits, int dtype,
+                                  size_t batch, size_t num_beams, size_t vocab, size_t ld,
+                                  const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+                                  const double* d_beam_scores, const double* d_uniforms,
+                                  size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores,
+                                  int32_t* d_out_status, uint32_t* d_out_flags, tc_stream stream);
+
 /* qwen building blocks on f32 [rows, ld] (d_in may equal d_out).
  * tc_apply_repetition_penalty builds its [V] mask in the context's workspace. */
 int tc_apply_repetition_penalty(tc_ctx* ctx, const float* d_in, float* d_out, size_t rows, size_t vocab,

@@ -27,7 +27,7 @@ EXPORTS = (
     "tc_create", "tc_destroy", "tc_sample", "tc_apply_repetition_penalty",
     "tc_apply_repetition_penalty_with_mask", "tc_build_suppression_mask",
     "tc_apply_token_suppression_with_mask", "tc_update_penalty_mask", "tc_greedy_sample",
-    "tc_last_error", "tc_abi_version", "tc_indextts_beam_step",
+    "tc_last_error", "tc_abi_version", "tc_indextts_beam_step", "tc_indextts_beam_step_noalloc",
 )
 
 
@@ -105,6 +105,9 @@ def load(path: str = LIB_PATH):
     L.tc_indextts_beam_step.restype = C.c_int
     L.tc_indextts_beam_step.argtypes = [vp, C.POINTER(SampleParams), vp, C.c_int, sz, sz, sz, sz, vp, vp, vp, vp,
                                         sz, vp, vp, vp, vp, vp]
+    L.tc_indextts_beam_step_noalloc.restype = C.c_int
+    L.tc_indextts_beam_step_noalloc.argtypes = [C.POINTER(SampleParams), vp, C.c_int, sz, sz, sz, sz, vp, vp, vp,
+                                                vp, sz, vp, vp, vp, vp, vp]
     L.tc_last_error.restype = C.c_char_p
     L.tc_last_error.argtypes = []
     L.tc_abi_version.restype = C.c_int

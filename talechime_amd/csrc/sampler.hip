@@ -29,6 +29,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/talechime_hip.h"
@@ -3244,6 +3245,93 @@ TC_DEFINE_LAUNCH(k_nano)
 
 }  // namespace
 
+// The beam step's row-pass workspace: per row kBeamCap kept ids, scores,
+// probabilities and top-k ids, then the counts, statuses and flags.  The
+// context's copy is allocated on its first beam step, behind R zero uniforms
+// (the row pass's own draw is not used); the allocation-free entry point keeps
+// it in the file-scope `scratch` array below.
+struct BeamWs {
+  uint32_t* keep_ids;
+  float* keep_scores;
+  float* keep_probs;
+  uint32_t* topk_ids;
+  uint32_t* topk_count;
+  uint32_t* keep_count;
+  uint32_t* ids;
+  int32_t* status;
+  uint32_t* flags;
+};
+
+static constexpr size_t beam_ws_bytes(size_t R) { return R * (size_t)tc::kBeamCap * 16 + R * 20; }
+
+static BeamWs beam_ws(void* base, size_t R) {
+  const size_t C = (size_t)tc::kBeamCap;
+  char* p = static_cast<char*>(base);
+  BeamWs w;
+  w.keep_ids = reinterpret_cast<uint32_t*>(p);
+  p += R * C * 4;
+  w.keep_scores = reinterpret_cast<float*>(p);
+  p += R * C * 4;
+  w.keep_probs = reinterpret_cast<float*>(p);
+  p += R * C * 4;
+  w.topk_ids = reinterpret_cast<uint32_t*>(p);
+  p += R * C * 4;
+  w.topk_count = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.keep_count = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.ids = reinterpret_cast<uint32_t*>(p);
+  p += R * 4;
+  w.status = reinterpret_cast<int32_t*>(p);
+  p += R * 4;
+  w.flags = reinterpret_cast<uint32_t*>(p);
+  return w;
+}
+
+// Allocation-free beam step: its row-pass workspace for up to kStaticBeamRows
+// beam rows (4.2 MB) in a file-scope device array, and the zero uniforms in a
+// second one that nothing ever writes.  Each GPU holds its own copy of both
+// for the life of the process; host code reaches them only through the
+// addresses hipGetSymbolAddress returns for the current device.
+namespace tc {
+constexpr int kStaticBeamRows = 256;
+constexpr int kMaxDevices = 64;
+}  // namespace tc
+static_assert(tc::kStaticBeamRows == TC_NOALLOC_BEAM_ROWS, "header and library agree on the static workspace");
+static __device__ __align__(256) unsigned char scratch[beam_ws_bytes(tc::kStaticBeamRows)];
+static __device__ __align__(256) double static_zero_uniforms[tc::kStaticBeamRows];
+
+namespace {
+struct StaticWs {
+  bool ready = false;
+  void* scratch = nullptr;
+  const double* zeros = nullptr;
+};
+StaticWs g_static[tc::kMaxDevices];
+std::mutex g_static_mu;
+
+// Resolves the two arrays' addresses on `device` (made current by the
+// caller), once per device.
+int static_ws_setup(int device, StaticWs* out) {
+  if (device < 0 || device >= tc::kMaxDevices) return fail(TC_EINVAL, "device %d out of range", device);
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  StaticWs& w = g_static[device];
+  if (!w.ready) {
+    void* sp = nullptr;
+    void* zp = nullptr;
+    hipError_t e = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    e = hipGetSymbolAddress(&zp, HIP_SYMBOL(static_zero_uniforms));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(static_zero_uniforms)");
+    w.scratch = sp;
+    w.zeros = static_cast<const double*>(zp);
+    w.ready = true;
+  }
+  *out = w;
+  return TC_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* tc_last_error(void) { return g_err.c_str(); }
@@ -3259,6 +3347,9 @@ int tc_create(int device, size_t max_rows, size_t max_vocab, tc_ctx** out) {
   if (device < 0 || device >= n) return fail(TC_EINVAL, "tc_create: device %d of %d", device, n);
   if (max_vocab == 0 || max_vocab > (size_t)INT32_MAX) return fail(TC_EINVAL, "tc_create: bad max_vocab");
   DeviceGuard g(device);
+  StaticWs sw;  // the allocation-free beam step's arrays on this device
+  int rc = static_ws_setup(device, &sw);
+  if (rc != TC_OK) return rc;
   tc_ctx* c = new tc_ctx{device, max_rows, max_vocab, nullptr, nullptr};
   e = hipMalloc(&c->d_mask, max_vocab);
   if (e != hipSuccess) {
@@ -3279,11 +3370,11 @@ void tc_destroy(tc_ctx* ctx) {
 
 // tc_sample; keep_scores (indextts only, with verify outputs) also receives
 // the final score of each kept id.
-static int sample_impl(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t rows,
-                       size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, const void* d_logits, int dtype,
+                       size_t rows, size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
                        const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
                        const tc_verify_out* verify, float* keep_scores, tc_stream stream) {
-  if (!ctx || !p) return fail(TC_EINVAL, "tc_sample: ctx/params is NULL");
+  if (!p) return fail(TC_EINVAL, "tc_sample: params is NULL");
   if (rows == 0) return TC_OK;
   if (!d_logits || !d_out_ids || !d_uniforms) return fail(TC_EINVAL, "tc_sample: NULL device pointer");
   if (dtype != TC_F32 && dtype != TC_BF16) return fail(TC_EINVAL, "tc_sample: dtype %d", dtype);
@@ -3397,13 +3488,13 @@ static int sample_impl(tc_ctx* ctx, const tc_sample_params* p, const void* d_log
     default:
       return fail(TC_EINVAL, "tc_sample: variant %d", p->variant);
   }
-  if ((size_t)V > ctx->max_vocab) return fail(TC_EINVAL, "tc_sample: vocab %d > context max %zu", V, ctx->max_vocab);
+  if ((size_t)V > max_vocab) return fail(TC_EINVAL, "tc_sample: vocab %d > context max %zu", V, max_vocab);
   int items = 0, threads = 0;
   if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg) {
     // qwen over bf16 rows up to kLargeVocab: the large-vocabulary kernel
     if (p->variant == TC_QWEN && dtype == TC_BF16 && V <= tc::kLargeVocab && p->hist_mode != TC_HIST_MASK &&
         !p->d_add_mask && (a.K >= 1 || a.greedy) && a.K <= tc::kLargeCand) {
-      DeviceGuard g(ctx->device);
+      DeviceGuard g(device);
       hipLaunchKernelGGL(tc::k_qwen_large, dim3((unsigned)rows), dim3(tc::kLargeThreads), 0,
                          reinterpret_cast<hipStream_t>(stream), a);
       hipError_t e = hipGetLastError();
@@ -3411,7 +3502,7 @@ static int sample_impl(tc_ctx* ctx, const tc_sample_params* p, const void* d_log
     }
     return fail(TC_EUNSUPPORTED, "tc_sample: vocab %d exceeds the register-resident kernel", V);
   }
-  DeviceGuard g(ctx->device);
+  DeviceGuard g(device);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e;
   switch (p->variant) {
@@ -3429,86 +3520,21 @@ int tc_sample(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int 
               size_t vocab, size_t ld, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
               const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
               const tc_verify_out* verify, tc_stream stream) {
-  return sample_impl(ctx, p, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, d_uniforms, d_out_ids,
-                     d_out_status, d_out_flags, verify, nullptr, stream);
+  if (!ctx) return fail(TC_EINVAL, "tc_sample: ctx is NULL");
+  return sample_impl(ctx->device, ctx->max_vocab, p, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids,
+                     d_uniforms, d_out_ids, d_out_status, d_out_flags, verify, nullptr, stream);
 }
 
-// The beam step's row-pass workspace, allocated on the context's first beam
-// step: per row kBeamCap kept ids, scores, probabilities and top-k ids, the
-// counts, statuses and flags, and a zero uniform per row (the row pass's own
-// draw is not used).
-struct BeamWs {
-  uint32_t* keep_ids;
-  float* keep_scores;
-  float* keep_probs;
-  uint32_t* topk_ids;
-  uint32_t* topk_count;
-  uint32_t* keep_count;
-  uint32_t* ids;
-  int32_t* status;
-  uint32_t* flags;
-  double* zero_u;
-};
-
-static BeamWs beam_ws(void* base, size_t R) {
-  const size_t C = (size_t)tc::kBeamCap;
-  char* p = static_cast<char*>(base);
-  BeamWs w;
-  w.zero_u = reinterpret_cast<double*>(p);
-  p += R * 8;
-  w.keep_ids = reinterpret_cast<uint32_t*>(p);
-  p += R * C * 4;
-  w.keep_scores = reinterpret_cast<float*>(p);
-  p += R * C * 4;
-  w.keep_probs = reinterpret_cast<float*>(p);
-  p += R * C * 4;
-  w.topk_ids = reinterpret_cast<uint32_t*>(p);
-  p += R * C * 4;
-  w.topk_count = reinterpret_cast<uint32_t*>(p);
-  p += R * 4;
-  w.keep_count = reinterpret_cast<uint32_t*>(p);
-  p += R * 4;
-  w.ids = reinterpret_cast<uint32_t*>(p);
-  p += R * 4;
-  w.status = reinterpret_cast<int32_t*>(p);
-  p += R * 4;
-  w.flags = reinterpret_cast<uint32_t*>(p);
-  return w;
-}
-
-static size_t beam_ws_bytes(size_t R) { return R * 8 + R * (size_t)tc::kBeamCap * 16 + R * 20; }
-
-int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
+// The beam step over a workspace `ws` of `ws_rows` rows and `zero_u` (>= rows
+// zero f64 uniforms); `device` is current.
+static int beam_step_impl(int device, size_t max_vocab, void* ws, size_t ws_rows, const double* zero_u,
+                          const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
                           size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
                           const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
                           size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
                           uint32_t* d_out_flags, tc_stream stream) {
-  if (!ctx || !p) return fail(TC_EINVAL, "tc_indextts_beam_step: ctx/params is NULL");
-  if (p->variant != TC_INDEXTTS) return fail(TC_EINVAL, "tc_indextts_beam_step: variant must be TC_INDEXTTS");
-  if (batch == 0) return TC_OK;
-  if (!d_logits || !d_beam_scores || !d_uniforms || !d_cand_flat || !d_cand_scores || !d_out_status)
-    return fail(TC_EINVAL, "tc_indextts_beam_step: NULL device pointer");
-  if (num_beams == 0 || num_beams > (size_t)tc::kBeamMaxBeams)
-    return fail(TC_EINVAL, "tc_indextts_beam_step: num_beams %zu (1..%d)", num_beams, tc::kBeamMaxBeams);
-  if (n_draws == 0 || n_draws > (size_t)tc::kBeamMaxDraws)
-    return fail(TC_EINVAL, "tc_indextts_beam_step: n_draws %zu (1..%d)", n_draws, tc::kBeamMaxDraws);
-  if (vocab == 0 || vocab > (size_t)INT32_MAX || num_beams * vocab > (size_t)UINT32_MAX)
-    return fail(TC_EINVAL, "tc_indextts_beam_step: num_beams * vocab must fit 32 bits");
-  if (batch > (size_t)INT32_MAX / num_beams) return fail(TC_EINVAL, "tc_indextts_beam_step: batch too large");
   const size_t rows = batch * num_beams;
-  if (rows > ctx->max_rows) return fail(TC_EINVAL, "tc_indextts_beam_step: %zu rows > context max %zu", rows, ctx->max_rows);
-  DeviceGuard g(ctx->device);
-  if (!ctx->d_beam) {
-    const size_t bytes = beam_ws_bytes(ctx->max_rows);
-    hipError_t e = hipMalloc(&ctx->d_beam, bytes);
-    if (e != hipSuccess) {
-      ctx->d_beam = nullptr;
-      return fail(TC_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-    }
-    e = hipMemset(ctx->d_beam, 0, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMemset");
-  }
-  const BeamWs w = beam_ws(ctx->d_beam, ctx->max_rows);
+  const BeamWs w = beam_ws(ws, ws_rows);
   tc_verify_out v{};
   v.cap = (uint32_t)tc::kBeamCap;
   v.d_topk_count = w.topk_count;
@@ -3519,8 +3545,8 @@ int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_
   v.d_norm = nullptr;
   tc_sample_params rp = *p;
   rp.d_mark_mask = nullptr;
-  int rc = sample_impl(ctx, &rp, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, w.zero_u, w.ids,
-                       w.status, w.flags, &v, w.keep_scores, stream);
+  int rc = sample_impl(device, max_vocab, &rp, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, zero_u,
+                       w.ids, w.status, w.flags, &v, w.keep_scores, stream);
   if (rc != TC_OK) return rc;
   tc::BeamArgs b{};
   b.nb = (int)num_beams;
@@ -3540,6 +3566,81 @@ int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_
   hipLaunchKernelGGL(tc::k_beam_joint, dim3((unsigned)batch), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), b);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TC_OK : hip_fail(e, "tc_indextts_beam_step launch");
+}
+
+// Argument checks shared by both beam entry points.
+static int beam_check(const char* fn, const tc_sample_params* p, const void* d_logits, size_t batch,
+                      size_t num_beams, size_t vocab, const double* d_beam_scores, const double* d_uniforms,
+                      size_t n_draws, const uint32_t* d_cand_flat, const double* d_cand_scores,
+                      const int32_t* d_out_status) {
+  if (!p) return fail(TC_EINVAL, "%s: params is NULL", fn);
+  if (p->variant != TC_INDEXTTS) return fail(TC_EINVAL, "%s: variant must be TC_INDEXTTS", fn);
+  if (batch == 0) return TC_OK;
+  if (!d_logits || !d_beam_scores || !d_uniforms || !d_cand_flat || !d_cand_scores || !d_out_status)
+    return fail(TC_EINVAL, "%s: NULL device pointer", fn);
+  if (num_beams == 0 || num_beams > (size_t)tc::kBeamMaxBeams)
+    return fail(TC_EINVAL, "%s: num_beams %zu (1..%d)", fn, num_beams, tc::kBeamMaxBeams);
+  if (n_draws == 0 || n_draws > (size_t)tc::kBeamMaxDraws)
+    return fail(TC_EINVAL, "%s: n_draws %zu (1..%d)", fn, n_draws, tc::kBeamMaxDraws);
+  if (vocab == 0 || vocab > (size_t)INT32_MAX || num_beams * vocab > (size_t)UINT32_MAX)
+    return fail(TC_EINVAL, "%s: num_beams * vocab must fit 32 bits", fn);
+  if (batch > (size_t)INT32_MAX / num_beams) return fail(TC_EINVAL, "%s: batch too large", fn);
+  return TC_OK;
+}
+
+int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
+                          size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
+                          const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
+                          size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
+                          uint32_t* d_out_flags, tc_stream stream) {
+  if (!ctx) return fail(TC_EINVAL, "tc_indextts_beam_step: ctx is NULL");
+  int rc = beam_check("tc_indextts_beam_step", p, d_logits, batch, num_beams, vocab, d_beam_scores, d_uniforms,
+                      n_draws, d_cand_flat, d_cand_scores, d_out_status);
+  if (rc != TC_OK || batch == 0) return rc;
+  const size_t rows = batch * num_beams;
+  if (rows > ctx->max_rows) return fail(TC_EINVAL, "tc_indextts_beam_step: %zu rows > context max %zu", rows, ctx->max_rows);
+  DeviceGuard g(ctx->device);
+  const size_t R = ctx->max_rows;
+  if (!ctx->d_beam) {
+    const size_t bytes = R * 8 + beam_ws_bytes(R);
+    hipError_t e = hipMalloc(&ctx->d_beam, bytes);
+    if (e != hipSuccess) {
+      ctx->d_beam = nullptr;
+      return fail(TC_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    e = hipMemset(ctx->d_beam, 0, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset");
+  }
+  const double* zero_u = static_cast<const double*>(ctx->d_beam);
+  void* ws = static_cast<char*>(ctx->d_beam) + R * 8;
+  return beam_step_impl(ctx->device, ctx->max_vocab, ws, R, zero_u, p, d_logits, dtype, batch, num_beams, vocab, ld,
+                        d_hist_off, d_hist_ids, d_beam_scores, d_uniforms, n_draws, d_cand_flat, d_cand_scores,
+                        d_out_status, d_out_flags, stream);
+}
+
+int tc_indextts_beam_step_noalloc(const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
+                                  size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
+                                  const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
+                                  size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores,
+                                  int32_t* d_out_status, uint32_t* d_out_flags, tc_stream stream) {
+  int rc = beam_check("tc_indextts_beam_step_noalloc", p, d_logits, batch, num_beams, vocab, d_beam_scores,
+                      d_uniforms, n_draws, d_cand_flat, d_cand_scores, d_out_status);
+  if (rc != TC_OK || batch == 0) return rc;
+  const size_t rows = batch * num_beams;
+  if (rows > (size_t)tc::kStaticBeamRows)
+    return fail(TC_EINVAL, "tc_indextts_beam_step_noalloc: %zu beam rows > the static workspace's %d", rows,
+                tc::kStaticBeamRows);
+  if (vocab > (size_t)tc::kMaxVocabReg)
+    return fail(TC_EUNSUPPORTED, "tc_indextts_beam_step_noalloc: vocab %zu > %d", vocab, tc::kMaxVocabReg);
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  StaticWs w;
+  rc = static_ws_setup(device, &w);
+  if (rc != TC_OK) return rc;
+  return beam_step_impl(device, (size_t)tc::kMaxVocabReg, w.scratch, (size_t)tc::kStaticBeamRows, w.zeros, p,
+                        d_logits, dtype, batch, num_beams, vocab, ld, d_hist_off, d_hist_ids, d_beam_scores,
+                        d_uniforms, n_draws, d_cand_flat, d_cand_scores, d_out_status, d_out_flags, stream);
 }
 
 static int grid_for(size_t n) {
