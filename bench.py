@@ -132,6 +132,7 @@ def parity_counts(ids, st, fl, o):
     return {"rows": int(ids.size), "both_ok": int(ok.sum()), "ids_equal": int((ok & (ids == o["ids"])).sum()),
             "status_mismatch": int((st != o["status"]).sum()), "unsupported": int((st == 7).sum()),
             "tie_cut_rows": int(tie.sum()), "near_tie_rows": int(near.sum()),
+            "exact_sum_rows": int(((fl & 32) != 0).sum()),
             "ids_differ_on_tie_rows": int((diff & (tie | near)).sum()),
             "ids_differ_elsewhere": int((diff & ~(tie | near)).sum())}
 

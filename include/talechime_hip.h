@@ -88,9 +88,12 @@ enum tc_flag {
                             uniform was used (the reference's StepRng advanced twice) */
   TC_FLAG_GREEDY = 4u,   /* qwen: temperature < 0.01, argmax, no uniform used */
   TC_FLAG_NAN_ROW = 8u,  /* qwen: NaN met at top-k (reference order unspecified) */
-  TC_FLAG_NEAR_TIE = 16u /* indextts: a top-p or draw decision lay within the f64 exp
+  TC_FLAG_NEAR_TIE = 16u, /* indextts: a top-p or draw decision lay within the f64 exp
                             error of the reference's libm (about 2^-46 relative); the
                             id follows this library's exp */
+  TC_FLAG_EXACT_SUM = 32u /* indextts without verification outputs: the row's decisions
+                             were not settled by the interval on the log-sum and took the
+                             exact sequential sum (informational; the id is the same) */
 };
 
 typedef struct tc_sample_params {

@@ -16,7 +16,7 @@ TC_OK, TC_EINVAL, TC_ENONFINITE, TC_ETOOFEW, TC_EHIP, TC_ENOMEM, TC_EDIST, TC_EU
 QWEN, COSY_RAS, INDEXTTS, MOSS, MOSS_NANO = range(5)
 F32, BF16 = 0, 1
 HIST_PER_ROW, HIST_BROADCAST, HIST_MASK = 0, 1, 2
-FLAG_TIE_CUT, FLAG_RAS, FLAG_GREEDY, FLAG_NAN_ROW, FLAG_NEAR_TIE = 1, 2, 4, 8, 16
+FLAG_TIE_CUT, FLAG_RAS, FLAG_GREEDY, FLAG_NAN_ROW, FLAG_NEAR_TIE, FLAG_EXACT_SUM = 1, 2, 4, 8, 16, 32
 
 STATUS_NAMES = {TC_OK: "ok", TC_EINVAL: "invalid argument", TC_ENONFINITE: "non-finite logits",
                 TC_ETOOFEW: "too few finite candidates", TC_EHIP: "HIP error", TC_ENOMEM: "out of memory",

@@ -1273,19 +1273,43 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       // log_softmax (generation.rs:95-105): d = x - max; S = sequential f32 sum of exp(d)
       float d[ITEMS], ap[ITEMS];
       uint32_t exm = 0, force = 0;
-      float mns = -__builtin_inff();
+      float mns = -__builtin_inff(), tsum = 0.0f;
+      // Without verification outputs the row is first decided from an
+      // interval on L (below), which needs only the sum: v_exp_f32 terms here,
+      // each within (2 |d| + 2) 2^-23 of exp(d) relative (the roundings of
+      // d log2 e and the instruction's own error).  Weighted by the terms
+      // (exp(d) |d| against a sum >= 1) that is below 2^-19 of the sum for any
+      // row of up to 16384 logits; with the f32 thread and wave sums the
+      // prediction is within 2^-16 more than seq_tau of the sequential sum.
+      // The exact sum's terms are computed only when the interval does not
+      // settle the row.
+      const bool cert_mode = !a.topk_count;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) {
         const bool v = (vm >> i) & 1u;
         d[i] = x[i] - mx;
         if (v && !((seen >> i) & 1ull)) mns = mns > d[i] ? mns : d[i];
-        ap[i] = v ? exp_approx(d[i]) : 0.0f;
-        exm |= (v ? 0u : 1u) << i;
-        force |= (v && !(d[i] >= -87.0f) ? 1u : 0u) << i;  // below the approximation's range
+        if (cert_mode) tsum += v ? __builtin_amdgcn_exp2f(d[i] * 1.44269504088896341f) : 0.0f;
       }
       if (mns > -16.0f) atomicAdd(&F.bins[(uint32_t)(-mns * 4.0f)], 1u);
       SeqSum<ITEMS> sq;
-      sq.predict(ap, F.seq);
+      // the exact sum's approximate terms and their prediction (SeqSum)
+      auto exact_terms = [&]() {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i) {
+          const bool v = (vm >> i) & 1u;
+          ap[i] = v ? exp_approx(d[i]) : 0.0f;
+          exm |= (v ? 0u : 1u) << i;
+          force |= (v && !(d[i] >= -87.0f) ? 1u : 0u) << i;  // below the approximation's range
+        }
+        sq.predict(ap, F.seq);
+      };
+      if (cert_mode) {
+        const float tw = dpp_wave_sum(tsum);
+        if (lane_id() == 0) F.seq.wsum[wave_id()] = tw;
+      } else {
+        exact_terms();
+      }
       lds_barrier();
       // Candidates, staged while the exact sum is finished.  The histogram of
       // per-thread maxima of d over ids not in the history puts the K-th largest
@@ -1299,6 +1323,15 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       const float Sp = sq.total(F.seq);
       const uint32_t cum = dpp_scan_u32(F.bins[lane_id()]);
       const uint64_t reach = __ballot(cum >= (uint32_t)a.K);
+      // An interval [Llo, Lhi] that holds log_sum: the reference's sequential
+      // sum S lies within seq_tau(V) of the prediction Sp (2^-16 more for the
+      // v_exp_f32 terms and their sums), and log_sum is glibc's logf(S),
+      // within an ulp of log S; v_log_f32 is within a few ulps of log2, and
+      // the slack covers both.
+      const float tt = seq_tau(V) + (cert_mode ? 0x1p-16f : 0.0f);
+      const float s_lo = Sp * (1.0f - tt), s_hi = Sp * (1.0f + tt);
+      const float Llo = __logf(s_lo) * (1.0f - 0x1p-18f) - 0x1p-20f;
+      const float Lhi = __logf(s_hi) * (1.0f + 0x1p-18f) + 0x1p-20f;
       float thr_d = __builtin_inff(), thr_s = __builtin_inff();
       if (reach) {
         const uint32_t b0 = (uint32_t)__builtin_ctzll(reach);
@@ -1308,12 +1341,10 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
         // taken a margin far above its roundings lower
         thr_s = -__builtin_inff();
         if (a.do_pen && a.pen_f > 0.0f) {
-          const float tt = seq_tau(V);
-          const float L_lo = __logf(Sp * (1.0f - tt)) - 1e-3f, L_hi = __logf(Sp * (1.0f + tt)) + 1e-3f;
+          const float L_lo = Llo - 1e-3f, L_hi = Lhi + 1e-3f;
           thr_s = L_lo + (thr_d - L_hi) / a.pen_f - 0x1p-9f;
         }
       }
-      sq.classify(ap, exm, force, e0, F.seq);
       // one compare per element against the lower threshold; the few hits are
       // then held to their own
       uint32_t sel = 0;
@@ -1334,10 +1365,37 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       wave_table_u32(F.wcand, &off, &n);
       off += ci - c;
       const bool stage = reach && n <= (uint32_t)FinLds::kCap;
-      // the list and the candidates in one pass over the elements
-      const bool listed_ok = sq.write_list(ap, d, e0, F.seq, stage ? sel : 0u, [&](int i) {
+      auto put_cand = [&](int i) {
         F.fin.cand[off++] = ((uint64_t)f2u(d[i]) << 32) | (((seen >> i) & 1ull) ? 0x80000000u : 0u) | (uint32_t)(e0 + i);
-      });
+      };
+      // idx_cert_finish writes the id when every L in [Llo, Lhi] gives it;
+      // otherwise (and with verification outputs) the exact sum below.
+      const bool cert = stage && cert_mode;
+      if (cert) {
+#pragma unroll
+        for (int i = 0; i < ITEMS; ++i)
+          if ((sel >> i) & 1u) put_cand(i);
+        lds_barrier();
+        if (wave_id() == 0) {
+          bool done = false;
+          if (s_lo > 1.0009765625f && s_hi < 1.0e30f) {
+            const float La = __logf(Sp);
+            done = idx_cert_finish(a, row, n, La < Llo ? Llo : (La > Lhi ? Lhi : La), Llo, Lhi, F.fin);
+          }
+          if (lane_id() == 0) F.fin.done = done ? 1u : 0u;
+        }
+        lds_barrier();
+        if (F.fin.done) return;
+      }
+      if (cert_mode) {
+        exact_terms();
+        lds_barrier();
+      }
+      sq.classify(ap, exm, force, e0, F.seq);
+      lds_barrier();
+      // the list (and, when not staged above, the candidates) in one pass over
+      // the elements
+      const bool listed_ok = sq.write_list(ap, d, e0, F.seq, stage && !cert ? sel : 0u, put_cand);
       // the exception keys of glibc logf around the expected sum, in flight
       // while the sum is finished
       LogfKeys lk;
@@ -1373,7 +1431,7 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
         if (wave_id() == 0) {
           const float L = logf_glibc_near(S, F.fref, F.lnref, F.invref, lk);
           put_norm(a, row, L);
-          idx_fast_finish(a, row, n, L, F.fin);
+          idx_fast_finish(a, row, n, L, F.fin, cert ? (uint32_t)TC_FLAG_EXACT_SUM : 0u);
         }
         return;
       }

@@ -506,7 +506,71 @@ struct FinLds {
   uint64_t rkey[kCap + 4];  // rank keys, zero padded
   double wr[kCap];          // top-p weights by ascending position (rank ns-1-p)
   float wr32[kCap];         // the same in f32 (the first, f32 decisions)
+  // by rank, for the interval finish: d, the separation its order needs
+  // (in wr32) and the history bit
+  float cd[kCap];
+  alignas(16) uint32_t k32[kCap + 4];  // 32-bit score keys by candidate, zero padded
+  uint8_t cpen[kCap];
+  uint32_t done;  // the interval finish decided the row
 };
+
+// Rank of each lane's key among n keys in LDS (zero padded to a multiple of
+// 4): the number of keys larger than it.
+template <int NS>
+__device__ __forceinline__ void fin_ranks(const uint64_t* rkey, uint32_t n, const uint64_t (&key)[2], uint32_t* rk0,
+                                          uint32_t* rk1) {
+  const uint32_t nr = (n + 3u) & ~3u;
+  uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+  if (NS == 1) {
+    for (uint32_t j = 0; j < nr; j += 4) {
+      a0 += rkey[j] > key[0] ? 1u : 0u;
+      a1 += rkey[j + 1] > key[0] ? 1u : 0u;
+      a2 += rkey[j + 2] > key[0] ? 1u : 0u;
+      a3 += rkey[j + 3] > key[0] ? 1u : 0u;
+    }
+    *rk0 = (a0 + a1) + (a2 + a3);
+    *rk1 = 0;
+  } else {
+    uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+    for (uint32_t j = 0; j < nr; j += 4) {
+      const uint64_t k0 = rkey[j], k1 = rkey[j + 1], k2 = rkey[j + 2], k3 = rkey[j + 3];
+      a0 += k0 > key[0] ? 1u : 0u;
+      a1 += k1 > key[0] ? 1u : 0u;
+      a2 += k2 > key[0] ? 1u : 0u;
+      a3 += k3 > key[0] ? 1u : 0u;
+      b0 += k0 > key[1] ? 1u : 0u;
+      b1 += k1 > key[1] ? 1u : 0u;
+      b2 += k2 > key[1] ? 1u : 0u;
+      b3 += k3 > key[1] ? 1u : 0u;
+    }
+    *rk0 = (a0 + a1) + (a2 + a3);
+    *rk1 = (b0 + b1) + (b2 + b3);
+  }
+}
+
+// Ranks from 32-bit keys (4 per LDS read): the number of larger keys and the
+// number of equal ones (itself included; a repeated key needs the 64-bit
+// ranks, which break the tie by position).
+template <int NS>
+__device__ __forceinline__ void fin_ranks32(const uint32_t* k32, uint32_t n, const uint32_t (&key)[2], uint32_t* rk0,
+                                            uint32_t* rk1, uint32_t* eq0, uint32_t* eq1) {
+  const uint32_t nr = (n + 3u) & ~3u;
+  const uint4* k4 = reinterpret_cast<const uint4*>(k32);
+  uint32_t g0 = 0, g1 = 0, e0 = 0, e1 = 0;
+  for (uint32_t j = 0; j < nr; j += 4) {
+    const uint4 v = k4[j >> 2];
+    g0 += (v.x > key[0] ? 1u : 0u) + (v.y > key[0] ? 1u : 0u) + (v.z > key[0] ? 1u : 0u) + (v.w > key[0] ? 1u : 0u);
+    e0 += (v.x == key[0] ? 1u : 0u) + (v.y == key[0] ? 1u : 0u) + (v.z == key[0] ? 1u : 0u) + (v.w == key[0] ? 1u : 0u);
+    if (NS == 2) {
+      g1 += (v.x > key[1] ? 1u : 0u) + (v.y > key[1] ? 1u : 0u) + (v.z > key[1] ? 1u : 0u) + (v.w > key[1] ? 1u : 0u);
+      e1 += (v.x == key[1] ? 1u : 0u) + (v.y == key[1] ? 1u : 0u) + (v.z == key[1] ? 1u : 0u) + (v.w == key[1] ? 1u : 0u);
+    }
+  }
+  *rk0 = g0;
+  *rk1 = g1;
+  *eq0 = e0;
+  *eq1 = e1;
+}
 
 // One-wave finish of an indextts row from its n (K <= n <= 128) candidates
 // (F.cand, vocabulary order, each with d = x - max and whether its id is in
@@ -526,7 +590,8 @@ struct FinLds {
 // decision falls inside it.
 // NS: the candidate slots per lane (1 when n <= 64; slot 1 then folds away).
 template <int NS>
-__device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
+__device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uint32_t n, float L, FinLds& F,
+                                                  uint32_t flags0) {
   const int lane = lane_id();
   float sc[2];
   uint32_t id[2];
@@ -550,34 +615,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   lds_wait();
   // rank = number of candidates with a larger key
   uint32_t rk0 = 0, rk1 = 0;
-  {
-    const uint32_t nr = (n + 3u) & ~3u;
-    uint32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0;
-    if (NS == 1) {
-      for (uint32_t j = 0; j < nr; j += 4) {
-        a0 += F.rkey[j] > key[0] ? 1u : 0u;
-        a1 += F.rkey[j + 1] > key[0] ? 1u : 0u;
-        a2 += F.rkey[j + 2] > key[0] ? 1u : 0u;
-        a3 += F.rkey[j + 3] > key[0] ? 1u : 0u;
-      }
-      rk0 = (a0 + a1) + (a2 + a3);
-    } else {
-      uint32_t b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-      for (uint32_t j = 0; j < nr; j += 4) {
-        const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1], k2 = F.rkey[j + 2], k3 = F.rkey[j + 3];
-        a0 += k0 > key[0] ? 1u : 0u;
-        a1 += k1 > key[0] ? 1u : 0u;
-        a2 += k2 > key[0] ? 1u : 0u;
-        a3 += k3 > key[0] ? 1u : 0u;
-        b0 += k0 > key[1] ? 1u : 0u;
-        b1 += k1 > key[1] ? 1u : 0u;
-        b2 += k2 > key[1] ? 1u : 0u;
-        b3 += k3 > key[1] ? 1u : 0u;
-      }
-      rk0 = (a0 + a1) + (a2 + a3);
-      rk1 = (b0 + b1) + (b2 + b3);
-    }
-  }
+  fin_ranks<NS>(F.rkey, n, key, &rk0, &rk1);
   const uint32_t rk[2] = {has[0] ? rk0 : 0xffffffffu, has[1] ? rk1 : 0xffffffffu};
   const uint32_t K = (uint32_t)a.K;
   const uint64_t bk0 = __ballot(rk[0] == K - 1), bk1 = __ballot(rk[1] == K - 1);
@@ -674,7 +712,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
       if (ok && !close) {
         const uint32_t tok = rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u));
         if (lane == 0) {
-          put_result(a, row, tok, TC_OK, 0u);
+          put_result(a, row, tok, TC_OK, flags0);
         }
         return;
       }
@@ -685,7 +723,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   double w[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) w[q] = surv[q] ? tc_exp_d((double)sc[q] - mxd) : 0.0;
-  uint32_t flags = 0;
+  uint32_t flags = flags0;
   // ---- top-p: ranks [r_cut, ns) are removed, except the min_keep first
   uint32_t r_cut = ns;
   if (a.do_topp) {
@@ -841,9 +879,291 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   }
 }
 
-__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, float L, FinLds& F) {
-  if (n <= (uint32_t)kWave) idx_fast_finish_t<1>(a, row, n, L, F);
-  else idx_fast_finish_t<2>(a, row, n, L, F);
+// The spacing of the floats in the binade of v (v > 0, normal): every real
+// of magnitude <= v rounds to a float within half of it.
+__device__ __forceinline__ float spacing_at(float v) { return u2f(f2u(v) & 0x7f800000u) * 0x1p-23f; }
+
+// The indextts finish decided without the exact log-sum: every L in
+// [Llo, Lhi] (an interval that holds the reference's log_sum) is shown to give
+// the same top-k set, the same top-p cut and the same draw, and the id is
+// written; false leaves the row to the exact path (nothing written).
+//
+// A candidate's score is s = fl(fl(fl(d - L) * c) / T) (c = pen for an id in
+// the history, else 1 and no multiply), so s = c (d - L) / T + eta with
+// |eta| <= r, r from the float spacings of |x'|, |x' pen| and |s| over the
+// interval; s is non-increasing in L.
+//   - Order.  Two ids outside the history whose d differ by more than
+//     ux + T us keep their order strictly for every L, and equal d stay
+//     tied; the sets cut at the top-k boundary and at the edge of the kept set
+//     are the same for every L when the pair across the cut is separated by
+//     three times that (an element on either side is within one separation of
+//     its neighbour at the cut).  An id in the history must keep its rank
+//     against every candidate: its score range [s(Lhi), s(Llo)] meets no other
+//     candidate's.
+//   - Weights.  With rank 0 as anchor, log w = s - s0 is
+//     (c (d - L) - c0 (d0 - L)) / T + eta - eta0: taken at La it is within
+//     delta = r + r0 + |c - c0| |L - La| / T of the reference's, plus the f32
+//     exp and the rounding of the log weight.  A top-p or draw test compares
+//     (1 - lim) A with lim B (A, B sums of weights); its margin is
+//     (1 - lim) sum(w delta) over A + lim sum(w delta) over B, plus the f32
+//     scans' rounding (2^-20 of the sums).
+template <int NS>
+__device__ __forceinline__ bool idx_cert_finish_t(const RowArgs& a, int row, uint32_t n, float La, float Llo,
+                                                  float Lhi, FinLds& F) {
+  const int lane = lane_id();
+  float sc[2], dd[2], slo[2] = {0.0f, 0.0f}, shi[2] = {0.0f, 0.0f};
+  uint32_t id[2];
+  bool has[2], pen[2];
+  uint64_t key[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t c = (uint32_t)(q * kWave + lane);
+    has[q] = q < NS && c < n;
+    const uint64_t v = has[q] ? F.cand[c] : 0ull;
+    id[q] = (uint32_t)v & 0x7fffffffu;
+    pen[q] = ((uint32_t)v & 0x80000000u) != 0u;
+    dd[q] = u2f((uint32_t)(v >> 32));
+    float xp = dd[q] - La;
+    xp = pen[q] ? xp * a.pen_f : xp;
+    sc[q] = a.do_temp ? xp / a.t_f : xp;
+    key[q] = has[q] ? (((uint64_t)tkey(sc[q]) << 32) | c) : 0ull;
+    if (q < NS) F.k32[c] = (uint32_t)(key[q] >> 32);
+  }
+  if (lane < 4) F.k32[NS * kWave + lane] = 0u;
+  // the score range over the interval, needed only when an id in the
+  // history is among the candidates
+  const bool anypen = __ballot((has[0] && pen[0]) || (has[1] && pen[1])) != 0ull;
+  if (anypen) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t c = (uint32_t)(q * kWave + lane);
+      float xh = dd[q] - Llo, xl = dd[q] - Lhi;
+      xh = pen[q] ? xh * a.pen_f : xh;
+      xl = pen[q] ? xl * a.pen_f : xl;
+      shi[q] = has[q] ? (a.do_temp ? xh / a.t_f : xh) : -__builtin_inff();
+      slo[q] = has[q] ? (a.do_temp ? xl / a.t_f : xl) : -__builtin_inff();
+      (void)c;
+    }
+  }
+  lds_wait();
+  uint32_t rk0 = 0, rk1 = 0, eq0 = 0, eq1 = 0;
+  {
+    const uint32_t k2[2] = {(uint32_t)(key[0] >> 32), (uint32_t)(key[1] >> 32)};
+    fin_ranks32<NS>(F.k32, n, k2, &rk0, &rk1, &eq0, &eq1);
+  }
+  if (__ballot((has[0] && eq0 > 1u) || (has[1] && eq1 > 1u))) {
+    // equal scores: ranks from the 64-bit keys (the later slot first)
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (q < NS) F.rkey[q * kWave + lane] = key[q];
+    if (lane < 4) F.rkey[NS * kWave + lane] = 0ull;
+    lds_wait();
+    fin_ranks<NS>(F.rkey, n, key, &rk0, &rk1);
+  }
+  const uint32_t rk[2] = {has[0] ? rk0 : 0xffffffffu, has[1] ? rk1 : 0xffffffffu};
+  // ids in the history keep their rank for every L: each one's score range,
+  // broadcast, meets no other candidate's
+  if (anypen) {
+    bool bad = false;
+#pragma unroll
+    for (int qp = 0; qp < 2; ++qp) {
+      for (uint64_t m = __ballot(has[qp] && pen[qp]); m; m &= m - 1ull) {
+        const int l = __builtin_ctzll(m);
+        const float plo = rl_f32(slo[qp], l), phi = rl_f32(shi[qp], l);
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          bad = bad || (has[q] && !(q == qp && lane == l) && !(slo[q] > phi || shi[q] < plo));
+      }
+    }
+    if (__ballot(bad)) return false;
+  }
+  const uint32_t K = (uint32_t)a.K;
+  const uint64_t bk0 = __ballot(rk[0] == K - 1), bk1 = __ballot(rk[1] == K - 1);
+  const float kth = bk0 ? rl_f32(sc[0], __builtin_ctzll(bk0)) : (bk1 ? rl_f32(sc[1], __builtin_ctzll(bk1)) : -__builtin_inff());
+  bool surv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) surv[q] = has[q] && !(sc[q] < kth);
+  const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
+  const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
+  const float T = a.do_temp ? a.t_f : 1.0f;
+  const float iT = (1.0f / T) * (1.0f + 0x1p-20f);  // >= 1/T: for bounds only
+  const float pn = a.pen_f;
+  // per candidate: the rounding bound r and the separation its order needs
+  float r[2], sep[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const float bx = (Lhi - dd[q]) * (1.0f + 0x1p-20f);
+    const float ux = spacing_at(bx);
+    float bs = bx, rx = 0.5f * ux;
+    if (pen[q]) {
+      bs = bx * pn * (1.0f + 0x1p-20f);
+      rx = 0.5f * (pn * ux + spacing_at(bs));
+    }
+    const float us = a.do_temp ? spacing_at(bs * iT * (1.0f + 0x1p-20f)) : 0.0f;
+    r[q] = (rx * iT + 0.5f * us) * (1.0f + 0x1p-20f);
+    sep[q] = 3.0f * (ux + T * us) * (1.0f + 0x1p-20f);
+    if (has[q] && rk[q] <= ns) {
+      F.cd[rk[q]] = dd[q];
+      F.cpen[rk[q]] = pen[q] ? 1 : 0;
+      F.wr32[rk[q]] = sep[q];
+    }
+  }
+  lds_wait();
+  // ok: the lane's candidate and the one ranked after it keep their order for
+  // every L, or either is an id in the history (whose rank was checked above)
+  bool ok[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    ok[q] = true;
+    if (has[q] && rk[q] < ns && rk[q] + 1u < n) {
+      const uint32_t p = rk[q] + 1u;
+      const float d1 = F.cd[p];
+      ok[q] = pen[q] || F.cpen[p] != 0 || dd[q] == d1 || dd[q] - d1 > F.wr32[p];
+    }
+  }
+  // the top-k cut: ranks K-1 .. ns-1 against their successors
+  if (__ballot((has[0] && rk[0] + 1u >= K && rk[0] < ns && !ok[0]) ||
+               (has[1] && rk[1] + 1u >= K && rk[1] < ns && !ok[1])))
+    return false;
+  // log weights against rank 0, in f64 from d (exact inputs), and their
+  // uncertainty delta
+  const uint64_t bm0 = __ballot(rk[0] == 0u), bm1 = __ballot(rk[1] == 0u);
+  const int l0 = bm0 ? __builtin_ctzll(bm0) : __builtin_ctzll(bm1);
+  const float d0 = bm0 ? rl_f32(dd[0], l0) : rl_f32(dd[1], l0);
+  const float r0 = bm0 ? rl_f32(r[0], l0) : rl_f32(r[1], l0);
+  const bool p0 = __builtin_amdgcn_readfirstlane(bm0 ? (pen[0] ? 1 : 0) : (pen[1] ? 1 : 0)) != 0;
+  const double c0 = p0 ? (double)pn : 1.0;
+  const double invT = 1.0 / (double)T;
+  const float hL = __builtin_fmaxf(La - Llo, Lhi - La);
+  float w[2], wd[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const double ci = pen[q] ? (double)pn : 1.0;
+    const double lw = (ci * ((double)dd[q] - (double)La) - c0 * ((double)d0 - (double)La)) * invT;
+    const float lf = (float)lw;
+    const float dlt = r[q] + r0 + (float)__builtin_fabs(ci - c0) * hL * iT + __builtin_fabsf(lf) * 0x1p-23f + 0x1p-20f;
+    w[q] = (surv[q] && lf >= -87.0f) ? exp_approx(lf) : 0.0f;
+    wd[q] = w[q] * dlt;
+  }
+  uint32_t rc = ns;
+  if (a.do_topp) {
+    // weights by ascending position ns-1-rank
+    float wa[2], da[2];
+    if (NS == 1) {
+      // one forward permute per value: survivors to their positions, the
+      // others to distinct lanes at or past ns
+      const int dst = (surv[0] ? (int)(ns - 1u - rk[0]) : (has[0] ? (int)rk[0] : lane)) << 2;
+      const float pw = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(w[0])));
+      const float pd = __int_as_float(__builtin_amdgcn_ds_permute(dst, __float_as_int(wd[0])));
+      wa[0] = (uint32_t)lane < ns ? pw : 0.0f;
+      da[0] = (uint32_t)lane < ns ? pd : 0.0f;
+      wa[1] = da[1] = 0.0f;
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        if (surv[q]) {
+          F.wr[ns - 1u - rk[q]] = (double)w[q];
+          F.rkey[ns - 1u - rk[q]] = (uint64_t)f2u(wd[q]);
+        }
+      lds_wait();
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t ap = (uint32_t)(q * kWave + lane);
+        const bool in = ap < ns;
+        wa[q] = in ? (float)F.wr[ap] : 0.0f;
+        da[q] = in ? u2f((uint32_t)F.rkey[ap]) : 0.0f;
+      }
+    }
+    const float cs0 = dpp_scan_f32(wa[0]);
+    const float ds0 = dpp_scan_f32(da[0]);
+    const float cs1 = NS == 2 ? dpp_scan_f32(wa[1]) + rl_f32(cs0, kWave - 1) : 0.0f;
+    const float ds1 = NS == 2 ? dpp_scan_f32(da[1]) + rl_f32(ds0, kWave - 1) : 0.0f;
+    const float sum = rl_f32(NS == 2 ? cs1 : cs0, kWave - 1);
+    const float dsum = rl_f32(NS == 2 ? ds1 : ds0, kWave - 1);
+    const float lim = (float)(1.0 - a.top_p_d);
+    const float limS = lim * sum;
+    const uint64_t rm0 = __ballot((uint32_t)lane < ns && cs0 <= limS);
+    const uint64_t rm1 = __ballot((uint32_t)(kWave + lane) < ns && cs1 <= limS);
+    const uint32_t n_rm = (uint32_t)(__popcll(rm0) + __popcll(rm1));
+    rc = ns - n_rm;
+    bool close = false;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t ap = (uint32_t)(q * kWave + lane);
+      const float cq = q == 0 ? cs0 : cs1, eq = q == 0 ? ds0 : ds1;
+      const float mg = ((1.0f - lim) * eq + lim * (dsum - eq) + 0x1p-20f * (cq + limS)) * 1.01f;
+      close = close || (ap < ns && (ap + 1u == n_rm || ap == n_rm) && __builtin_fabsf(cq - limS) <= mg);
+    }
+    if (__ballot(close)) return false;
+  }
+  const uint32_t live_r = rc > (uint32_t)a.min_keep ? rc : (uint32_t)a.min_keep;
+  // the edge of the kept set
+  if (live_r < ns && __ballot((has[0] && rk[0] + 1u == live_r && !ok[0]) || (has[1] && rk[1] + 1u == live_r && !ok[1])))
+    return false;
+  bool lv[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) lv[q] = surv[q] && rk[q] < live_r;
+  const uint64_t lm0 = __ballot(lv[0]), lm1 = __ballot(lv[1]);
+  const uint32_t nl = (uint32_t)(__popcll(lm0) + __popcll(lm1));
+  float e[2], ed[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    e[q] = lv[q] ? w[q] : 0.0f;
+    ed[q] = lv[q] ? wd[q] : 0.0f;
+  }
+  const float acc0 = dpp_scan_f32(e[0]);
+  const float acc1 = NS == 2 ? dpp_scan_f32(e[1]) + rl_f32(acc0, kWave - 1) : acc0;
+  const float sum2 = rl_f32(acc1, kWave - 1);
+  const float dacc0 = dpp_scan_f32(ed[0]);
+  const float dacc1 = NS == 2 ? dpp_scan_f32(ed[1]) + rl_f32(dacc0, kWave - 1) : dacc0;
+  const float dsum2 = rl_f32(dacc1, kWave - 1);
+  const float u = (float)reinterpret_cast<const double*>(a.uniforms)[row];
+  const float target = u * sum2;
+  const uint64_t pz0 = __ballot(lv[0] && e[0] > 0.0f), pz1 = __ballot(lv[1] && e[1] > 0.0f);
+  const uint64_t hit0 = __ballot(lv[0] && e[0] > 0.0f && acc0 > target);
+  const uint64_t hit1 = __ballot(lv[1] && e[1] > 0.0f && acc1 > target);
+  if (nl == 0u || (pz0 | pz1) == 0ull) return false;
+  uint32_t pick = 0;
+  bool found = true;
+  if (hit0) pick = (uint32_t)__builtin_ctzll(hit0);
+  else if (hit1) pick = 64u + (uint32_t)__builtin_ctzll(hit1);
+  else {
+    found = false;
+    pick = pz1 ? 64u + 63u - (uint32_t)__builtin_clzll(pz1) : 63u - (uint32_t)__builtin_clzll(pz0);
+  }
+  // acc_j > u sum2 is (1 - u) acc_j - u (sum2 - acc_j) > 0: its margin weighs
+  // the deltas of the two parts the same way
+  auto close_at = [&](uint32_t j) -> bool {
+    const float aj = rl_f32(j < 64 ? acc0 : acc1, (int)(j & 63u));
+    const float dj = rl_f32(j < 64 ? dacc0 : dacc1, (int)(j & 63u));
+    const float mg = ((1.0f - u) * dj + u * (dsum2 - dj) + 0x1p-20f * (aj + target)) * 1.01f;
+    return __builtin_fabsf(aj - target) <= mg;
+  };
+  bool close = close_at(pick);
+  if (found) {
+    const uint64_t below0 = pick < 64 ? (pz0 & ((1ull << pick) - 1ull)) : pz0;
+    const uint64_t below1 = pick < 64 ? 0ull : (pz1 & ((1ull << (pick - 64u)) - 1ull));
+    if (below1 || below0) {
+      const uint32_t prev = below1 ? 64u + 63u - (uint32_t)__builtin_clzll(below1) : 63u - (uint32_t)__builtin_clzll(below0);
+      close = close || close_at(prev);
+    }
+  }
+  if (close) return false;
+  const uint32_t tok = rl_u32(pick < 64 ? id[0] : id[1], (int)(pick & 63u));
+  if (lane == 0) put_result(a, row, tok, TC_OK, 0u);
+  return true;
+}
+
+__device__ __forceinline__ bool idx_cert_finish(const RowArgs& a, int row, uint32_t n, float La, float Llo, float Lhi,
+                                                FinLds& F) {
+  if (n <= (uint32_t)kWave) return idx_cert_finish_t<1>(a, row, n, La, Llo, Lhi, F);
+  return idx_cert_finish_t<2>(a, row, n, La, Llo, Lhi, F);
+}
+
+__device__ __forceinline__ void idx_fast_finish(const RowArgs& a, int row, uint32_t n, float L, FinLds& F,
+                                                uint32_t flags0 = 0u) {
+  if (n <= (uint32_t)kWave) idx_fast_finish_t<1>(a, row, n, L, F, flags0);
+  else idx_fast_finish_t<2>(a, row, n, L, F, flags0);
 }
 
 }  // namespace tc
