@@ -34,7 +34,6 @@
 
 #include "../../include/talechime_hip.h"
 #include "tc_device.h"
-#include "tc_select.h"
 #include "tc_seqsum.h"
 
 namespace tc {

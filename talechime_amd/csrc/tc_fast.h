@@ -8,7 +8,6 @@
 
 #include "tc_device.h"
 #include "tc_dpp.h"
-#include "tc_select.h"
 
 namespace tc {
 
@@ -628,7 +627,7 @@ __device__ __forceinline__ void idx_fast_finish_t(const RowArgs& a, int row, uin
   const uint64_t sm0 = __ballot(surv[0]), sm1 = __ballot(surv[1]);
   const uint32_t ns = (uint32_t)(__popcll(sm0) + __popcll(sm1));
   // ---- f32 decisions first (when no verification outputs are asked for):
-  // weights exp(x'' - max) by exp_approx, within 2.5 ulps of the reference's
+  // weights exp(x'' - max) by exp_approx, within 3 ulps of the reference's
   // f64 values (below 2^-87 they are taken as 0: under 2^-125 of the sum),
   // f32 tree sums and scans.  (ns + 32) * 2^-21 of a sum bounds the f32
   // weights, sums and scans and the reference's f64 sequential normalised
