@@ -1665,12 +1665,15 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
         const int q = q0 + u * bd;
         if (q >= nchunks) break;
         const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
-        bad |= c.bad ? 1u : 0u;
 #pragma unroll
         for (int h = 0; h < 8; ++h) {
           const int e = q * 8 - shift + h;
-          const uint64_t k = ((uint64_t)ckey(logit(c.x[h], (c.sn >> h) & 1u, e)) << 32) | (uint64_t)(~(uint32_t)e);
-          best = (e >= 0 && e < V && k > best) ? k : best;
+          const float lv = logit(c.x[h], (c.sn >> h) & 1u, e);
+          const bool in = e >= 0 && e < V;
+          // candle argmax skips NaN; a NaN at index 0 is never replaced
+          if (in && __builtin_isnan(lv)) bad |= e == 0 ? 2u : 1u;
+          const uint64_t k = ((uint64_t)ckey(lv) << 32) | (uint64_t)(~(uint32_t)e);
+          best = (in && !__builtin_isnan(lv) && k > best) ? k : best;
         }
       }
 #pragma unroll
@@ -1710,11 +1713,6 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     bad = bad2 ? 1u : 0u;
   }
   bad = block_or_u(bad, S.s);
-  if (bad) {  // NaN / inf: the reference's top-k takes its NaN path; not handled at this vocabulary
-    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
-    no_verify(a, row);
-    return;
-  }
   if (a.greedy) {  // candle argmax: first index whose value is strictly greater
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -1726,12 +1724,69 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     if (t == 0) {
       uint64_t b = 0;
       for (int w = 0; w < num_waves(); ++w) b = S.cand[w] > b ? S.cand[w] : b;
-      finish_row(a, row, b ? ~(uint32_t)(b & 0xffffffffu) : 0u, TC_OK, TC_FLAG_GREEDY);
+      finish_row(a, row, (b && !(bad & 2u)) ? ~(uint32_t)(b & 0xffffffffu) : 0u, TC_OK, TC_FLAG_GREEDY);
     }
     no_verify(a, row);
     return;
   }
-  kmax = block_max_u(kmax, S.s);
+  // Non-finite logits (rare): one more pass classifies them by their final
+  // logit.  A +inf logit survives top-k, makes every softmax weight NaN and
+  // sends the reference's CDF to index 0 (sampling.rs:302-328).  NaN logits
+  // take the reference's NaN path at top-k, whose order Rust leaves
+  // unspecified: they are left out here and the row is flagged; the largest
+  // key is then taken again without them.
+  bool row_nan = false;
+  uint32_t row_flags = 0;
+  if (bad) {
+    uint32_t pinf = 0, nan = 0, km = 0;
+    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = tb + kLargeU * t + u;
+        if (q >= nchunks) break;
+        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int e = q * 8 - shift + h;
+          if (e < 0 || e >= V) continue;
+          const bool sn = (c.sn >> h) & 1u;
+          const float lv = logit(c.x[h], sn, e);
+          nan |= __builtin_isnan(lv) ? 1u : 0u;
+          pinf |= lv == __builtin_inff() ? 1u : 0u;
+          const uint32_t bb = f2u(c.x[h]);
+          if (!sn && e != eos && !((bb & 0x7f800000u) == 0x7f800000u && (bb & 0x007fffffu) != 0u))
+            km = max(km, ckey(c.x[h]) >> 16);
+        }
+      }
+    });
+    pinf = block_or_u(pinf, S.s);
+    row_nan = block_or_u(nan, S.s) != 0u;
+    row_flags = row_nan ? (uint32_t)TC_FLAG_NAN_ROW : 0u;
+    if (pinf) {
+      finish_row(a, row, 0u, TC_OK, row_flags);
+      no_verify(a, row);
+      return;
+    }
+    kmax = block_max_u(km, S.s);
+  } else {
+    kmax = block_max_u(kmax, S.s);
+  }
+  // the ids whose (widened bf16) logit is NaN, bit h of a chunk
+  auto nan8 = [&](const uint4& v, int c0) -> uint32_t {
+    uint32_t m = 0;
+    if (row_nan) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      const uint32_t hb = bits_at_fn(S.bits, nwords, c0);
+#pragma unroll
+      for (int h = 0; h < 8; ++h) {
+        const int e = c0 + h;
+        const uint32_t b = (h & 1) ? (w[h >> 1] & 0xffff0000u) : (w[h >> 1] << 16);
+        const float lv = logit(__uint_as_float(b), ((hb >> h) & 1u) != 0u, e);
+        m |= (e >= 0 && e < V && __builtin_isnan(lv)) ? 1u << h : 0u;
+      }
+    }
+    return m;
+  };
   // pass B: exact histogram of the 256 keys at and below the largest
   // (two keys per 32-bit operation; a live key is at most kmax, so its
   // 16-bit distance below kmax does not wrap)
@@ -1747,7 +1802,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
       if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
       const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
-      const uint32_t live = inm & ~hb & ~em;
+      const uint32_t live = inm & ~hb & ~em & ~nan8(raw[u], c0);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, bkey16x2(u4_word(raw[u], j))));
@@ -1771,11 +1826,82 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     if (l == 0) S.misc[0] = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;
   }
   __syncthreads();
-  const uint32_t bK = S.misc[0];
-  if (bK == 0xffffffffu) {  // the K-th largest lies more than 256 keys below the largest
-    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
-    no_verify(a, row);
-    return;
+  uint32_t bK = S.misc[0];
+  if (bK == 0xffffffffu) {
+    // The K-th largest key lies more than 256 keys below the largest (peaked
+    // or shifted rows): a radix select over the full 16-bit distance, its
+    // high byte first (runs of equal bins added at once), then its low byte
+    // inside the chosen high-byte bin.
+    uint32_t lvl_hi = 0;
+    for (int lvl = 0; lvl < 2; ++lvl) {
+      if (t < 256) S.hist[t] = 0u;
+      __syncthreads();
+      tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+        uint32_t run_bin = 0xffffffffu, run_n = 0;
+#pragma unroll
+        for (int u = 0; u < kLargeU; ++u) {
+          const int q = tb + kLargeU * t + u;
+          if (q >= nchunks) break;
+          const int c0 = q * 8 - shift;
+          const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
+          uint32_t inm = 0xffu;
+          if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+          if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+          const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+          const uint32_t live = inm & ~hb & ~em & ~nan8(raw[u], c0);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              if (!((live >> (2 * j + hh)) & 1u)) continue;
+              const uint32_t dist = kmax - ((k2 >> (16 * hh)) & 0xffffu);
+              if (lvl == 1 && (dist >> 8) != lvl_hi) continue;
+              const uint32_t bin = lvl == 0 ? (dist >> 8) : (dist & 0xffu);
+              if (bin != run_bin) {
+                if (run_n) atomicAdd(&S.hist[run_bin], run_n);
+                run_bin = bin;
+                run_n = 0;
+              }
+              ++run_n;
+            }
+          }
+        }
+        if (run_n) atomicAdd(&S.hist[run_bin], run_n);
+      });
+      __syncthreads();
+      // the bin holding the K-th (the high level counts from the largest key;
+      // the low level counts what the higher bins left)
+      const uint32_t need = lvl == 0 ? K : S.misc[1];
+      if (wave_id() == 0) {
+        const int l = lane_id();
+        const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
+        const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
+        uint32_t b = 0xffffffffu, before = 0;
+        if (ex + h0 >= need) { b = 4 * l; before = ex; }
+        else if (ex + h0 + h1 >= need) { b = 4 * l + 1; before = ex + h0; }
+        else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
+        else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
+        const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
+        if (l == 0) {
+          const int w = m ? __builtin_ctzll(m) : 0;
+          S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
+          S.misc[1] = m ? need - rl_u32(before, w) : 0u;
+        }
+      }
+      __syncthreads();
+      if (S.misc[0] == 0xffffffffu) break;  // fewer than K ids outside the history
+      if (lvl == 0) lvl_hi = S.misc[0];
+      else bK = (lvl_hi << 8) | S.misc[0];
+      __syncthreads();
+    }
+    if (bK == 0xffffffffu) {
+      // fewer than K live ids (almost all in the history or excluded): every
+      // candidate must then be ranked, more than this kernel stages
+      finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
+      no_verify(a, row);
+      return;
+    }
   }
   const uint32_t keyK = kmax - bK;
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
@@ -1787,19 +1913,37 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   // reaches thr (0xff80, above every finite key, when none does).  Both zeros
   // share key 0x8000 and both give a logit of zero.  Every thread finds keyP
   // by the same bisection over the finite keys [0x0080, 0xff7f].
+  // A negative penalty makes the penalised logit non-increasing in the bf16
+  // value: then keyP is the largest finite key whose penalised logit reaches
+  // thr, the ids at or below it qualify, and pass C compares the complemented
+  // keys of those ids (0xffff - key) against 0xffff - keyP.
+  const bool rev = a.do_pen && a.pen_f < 0.0f;
+  auto pen_logit = [&](uint32_t key) {  // logit() of a penalised id that is not EOS
+    const uint32_t b = (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu);
+    const float x = __uint_as_float(b << 16);
+    float v = x * (x > 0.0f ? a.inv_pen : a.pen_f);
+    if (a.do_temp) v = v * a.tmul + 0.0f;
+    return v;
+  };
   uint32_t keyP = 0xff80u;
-  if (a.do_pen) {
+  if (a.do_pen && !rev) {
     uint32_t lo = 0x0080u, hi = 0xff80u;
     while (lo < hi) {
       const uint32_t mid = (lo + hi) >> 1;
-      const uint32_t b = (mid & 0x8000u) ? (mid & 0x7fffu) : (~mid & 0xffffu);
-      const float x = __uint_as_float(b << 16);
-      float v = x * (x > 0.0f ? a.inv_pen : a.pen_f);  // logit() for a penalised id that is not EOS
-      if (a.do_temp) v = v * a.tmul + 0.0f;
-      if (v >= thr) hi = mid;
+      if (pen_logit(mid) >= thr) hi = mid;
       else lo = mid + 1u;
     }
     keyP = lo;
+  } else if (rev) {
+    uint32_t lo = 0x0080u, hi = 0xff7fu;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1u) >> 1;
+      if (pen_logit(mid) >= thr) lo = mid;
+      else hi = mid - 1u;
+    }
+    // complemented threshold; 0xffff (no finite complemented key reaches it)
+    // when no penalised logit reaches thr
+    keyP = pen_logit(lo) >= thr ? (0xffffu - lo) : 0xffffu;
   }
   // pass C: candidates in vocabulary order, a tile at a time.  Live ids are
   // selected by key (two per instruction), penalised ones by the bitmap
@@ -1819,11 +1963,12 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
         if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
         if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
         const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
-        const uint32_t live = inm & ~hb & ~em, pen = inm & hb & ~em;
+        const uint32_t nm = nan8(raw[u], c0);
+        const uint32_t live = inm & ~hb & ~em & ~nm, pen = inm & hb & ~em & ~nm;
         uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
+          const uint32_t k2 = bkey16x2(u4_word(raw[u], j)) ^ (rev ? half_mask(pen, j) : 0u);
           const uint32_t th2 = kP32 ^ ((kK32 ^ kP32) & half_mask(live, j));
           const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2),
                                                                                      __builtin_bit_cast(u16x2, th2)));
@@ -1867,7 +2012,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   });
   __syncthreads();
   if (n_c > (uint32_t)kLargeCand) {
-    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
     no_verify(a, row);
     return;
   }
@@ -1882,7 +2027,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   for (int j = t; j < (int)n_c; j += blockDim.x) ns_part += (uint32_t)(S.cand[j] >> 32) <= kth_hi ? 1u : 0u;
   const uint32_t ns = block_sum_u(ns_part, S.s);
   const float vmax = val_of(S.cand[0]);
-  uint32_t flags = 0, cut = ns;
+  uint32_t flags = row_flags, cut = ns;
   if (a.do_topp) {
     // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential
     // sum, running sum of e / S, cutoff at the first crossing (kept)
@@ -3549,6 +3694,9 @@ static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, 
   int items = 0, threads = 0;
   if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg) {
     // qwen over bf16 rows up to kLargeVocab: the large-vocabulary kernel
+    if (p->variant == TC_QWEN && a.do_pen && (a.pen_f == 0.0f || !isfinite(a.pen_f)))
+      return fail(TC_EUNSUPPORTED, "tc_sample: repetition penalty %g above %d logits", p->repetition_penalty,
+                  tc::kMaxVocabReg);
     if (p->variant == TC_QWEN && dtype == TC_BF16 && V <= tc::kLargeVocab && p->hist_mode != TC_HIST_MASK &&
         !p->d_add_mask && (a.K >= 1 || a.greedy) && a.K <= tc::kLargeCand) {
       DeviceGuard g(device);

@@ -661,8 +661,84 @@ def test_qwen_large_vocab_greedy_broadcast_and_unsupported(sampler):
     assert (g["status"] == 0).all()
     tie = (o["flags"] & 1) != 0
     same(g, o, rows=[r for r in range(3) if not tie[r]])
-    # a NaN row is not handled at this vocabulary (the reference's NaN top-k order is unspecified)
+    # a NaN row: the reference's NaN top-k order is unspecified; the NaN ids
+    # are left out and the row is flagged
     y = x.copy()
     y[0, 5] = np.nan
     g, _ = run(sampler, O.QWEN, y[:1], None, [0.5], bf16=True, temperature=0.8, top_k=50, top_p=0.9, penalty=1.0)
-    assert g["status"][0] == _lib.TC_EUNSUPPORTED
+    assert g["status"][0] == 0 and g["flags"][0] & _lib.FLAG_NAN_ROW
+    assert np.isfinite(y[0, g["ids"][0]]) and g["ids"][0] != 5
+
+
+def _large_rows(kind, rows, V, g_):
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    if kind == "spiked":       # one logit far above the rest: the K-th lies many binades below
+        x[np.arange(rows), g_.integers(0, V, rows)] = np.float32(1000.0)
+    elif kind == "shifted":    # N(-10, 3^2): the top values straddle zero
+        x -= np.float32(10.0)
+    elif kind == "max_subtracted":
+        x -= x.max(axis=1, keepdims=True)
+    elif kind == "peaked":     # a few huge logits, the rest a long tail
+        x = np.where(g_.random((rows, V)) < 1e-4, x + 40, x).astype(np.float32)
+    return x
+
+
+@pytest.mark.parametrize("kind", ["spiked", "shifted", "max_subtracted", "peaked"])
+def test_qwen_large_vocab_keys_far_below_the_max(sampler, kind):
+    # the K-th largest key lies more than 256 bf16 keys below the largest:
+    # the kernel's full 16-bit radix select
+    V = 151936
+    g_ = np.random.default_rng(hash(kind) % 1000)
+    rows = 4
+    x = _large_rows(kind, rows, V, g_)
+    top = np.argsort(-x, axis=1)[:, :1200]
+    hist = [top[r, ::7].tolist() + g_.integers(0, V, 300).tolist() for r in range(rows)]
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.7, top_k=1000, top_p=0.95, penalty=1.1),
+               dict(temperature=1.0, top_k=300, top_p=0.99, penalty=1.0),
+               dict(temperature=0.9, top_k=64, top_p=1.0, penalty=2.0)):
+        print(f"[large] kind={kind} {kw}", flush=True)
+        g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+def test_qwen_large_vocab_negative_penalty(sampler):
+    # a negative penalty maps logits in reverse order (sampling.rs:388-395 does
+    # not reject it): penalised ids are selected by the reversed key threshold
+    V = 151936
+    g_ = np.random.default_rng(77)
+    rows = 4
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    low = np.argsort(x, axis=1)[:, :40]     # the most negative logits become the largest
+    top = np.argsort(-x, axis=1)[:, :40]
+    hist = [low[r].tolist() + top[r, ::2].tolist() + g_.integers(0, V, 200).tolist() for r in range(rows)]
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.7, top_k=50, top_p=0.9, penalty=-1.0),
+               dict(temperature=1.0, top_k=1000, top_p=0.95, penalty=-2.5)):
+        g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+def test_qwen_large_vocab_infinities(sampler):
+    # +inf (after the caller chain) sends the reference's CDF to index 0;
+    # -inf entries weigh zero; the EOS id forced to -inf masks a +inf there
+    V = 151936
+    g_ = np.random.default_rng(78)
+    x = (g_.standard_normal((4, V)) * 3).astype(np.float32)
+    x[0, 1234] = np.inf
+    x[1, g_.integers(0, V, 5000)] = -np.inf
+    x[2, 999] = np.inf     # the EOS id below: forced to -inf, so the row samples normally
+    x[3, 4321] = -np.inf
+    x[3, 4322] = np.inf    # penalised with a positive penalty: stays +inf
+    hist = [[1], [2], [3], [4322]]
+    g, o = run(sampler, O.QWEN, x, hist, g_.random(4), bf16=True, temperature=0.8, top_k=100, top_p=0.9,
+               penalty=1.2, eos_id=999)
+    assert (g["status"] == 0).all(), g["status"]
+    assert g["ids"][0] == 0 and o["ids"][0] == 0
+    assert g["ids"][3] == 0 and o["ids"][3] == 0
+    tie = (o["flags"] & 1) != 0
+    same(g, o, rows=[r for r in (1, 2) if not tie[r]])
