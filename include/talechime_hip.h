@@ -21,6 +21,7 @@
  *                            (generation.rs:280) with one draw per row
  *   tc_indextts_beam_step    crates/indextts/src/generation.rs:640-701, the joint scores
  *                            and sample_without_replacement of the beam-sample loop
+ *   tc_indextts_beam_search_step  generation.rs:671-679, the same loop with do_sample false
  *   tc_sample (TC_MOSS)      crates/moss-tts/src/sampling.rs:22 `sample`
  *   tc_sample (TC_MOSS_NANO) crates/moss-tts/src/nano/sampling.rs:11 `Sampler::sample`
  *   tc_apply_repetition_penalty            sampling.rs:334
@@ -187,6 +188,23 @@ int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* params, const voi
                           const double* d_beam_scores, const double* d_uniforms, size_t n_draws,
                           uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
                           uint32_t* d_out_flags, tc_stream stream);
+
+/*
+ * The same loop without sampling (GenerateConfig.do_sample = false): the beam-search
+ * branch of crates/indextts/src/generation.rs:671-679.  Each beam row keeps
+ * log_softmax and the repetition penalty only (the temperature, top-k and top-p of
+ * params are not applied, generation.rs:653-662); the candidates are the n_keep best
+ * joint scores score + beam score of each element over all num_beams * vocab flat
+ * indices, by score descending, equal scores in ascending flat order (the
+ * reference's stable sorts).  n_keep is 2 * num_beams in the reference, at most 64.
+ * d_cand_flat / d_cand_scores [batch * n_keep]; d_out_status [batch].  Shares the
+ * context's beam workspace with tc_indextts_beam_step.
+ */
+int tc_indextts_beam_search_step(tc_ctx* ctx, const tc_sample_params* params, const void* d_logits, int dtype,
+                                 size_t batch, size_t num_beams, size_t vocab, size_t ld,
+                                 const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+                                 const double* d_beam_scores, size_t n_keep, uint32_t* d_cand_flat,
+                                 double* d_cand_scores, int32_t* d_out_status, tc_stream stream);
 
 /*
  * tc_indextts_beam_step without any allocation.  No counterpart in the reference:

@@ -107,6 +107,8 @@ def lib():
         vp = C.c_void_p
         L.tco_idx_beam_step.restype = C.c_int
         L.tco_idx_beam_step.argtypes = [C.POINTER(Params), vp, sz, sz, sz, vp, vp, vp, vp, sz, vp, vp, vp]
+        L.tco_idx_beam_search_step.restype = C.c_int
+        L.tco_idx_beam_search_step.argtypes = [C.POINTER(Params), vp, sz, sz, sz, vp, vp, vp, sz, vp, vp]
         L.tco_cosy_nucleus.restype = C.c_uint32
         L.tco_cosy_nucleus.argtypes = [f32p, sz, C.c_float, sz, C.c_float, C.POINTER(C.c_int),
                                        u32p, f32p, u32p]
@@ -305,6 +307,29 @@ def idx_beam_step(params, logits, hist_off, hist_ids, beam_scores, num_beams, un
     if rc != OK:
         raise ValueError(f"tco_idx_beam_step: status {rc}")
     return {"flat": flat, "scores": sc, "status": st}
+
+
+def idx_beam_search_step(params, logits, hist_off, hist_ids, beam_scores, num_beams, n_keep):
+    """The do_sample = false branch (generation.rs:671-679): flat [batch, n_keep]
+    and scores, the n_keep best joint scores descending."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    rows, V = logits.shape
+    assert rows % num_beams == 0
+    batch = rows // num_beams
+    ho = None if hist_off is None else np.ascontiguousarray(hist_off, np.uint32)
+    hi = None if hist_ids is None else np.ascontiguousarray(hist_ids, np.uint32)
+    if hi is not None and hi.size == 0:
+        hi = np.zeros(1, np.uint32)
+    bs = np.ascontiguousarray(beam_scores, np.float64)
+    flat = np.zeros((batch, n_keep), np.uint32)
+    sc = np.zeros((batch, n_keep), np.float64)
+    rc = lib().tco_idx_beam_search_step(C.byref(params), logits.ctypes.data, batch, num_beams, V,
+                                        None if ho is None else ho.ctypes.data,
+                                        None if hi is None else hi.ctypes.data, bs.ctypes.data, n_keep,
+                                        flat.ctypes.data, sc.ctypes.data)
+    if rc != OK:
+        raise ValueError(f"tco_idx_beam_search_step: status {rc}")
+    return {"flat": flat, "scores": sc}
 
 
 def cosy_nucleus(probs, top_p, top_k, u0):

@@ -965,6 +965,58 @@ int tco_idx_beam_step(const tco_params* p, const float* logits, size_t batch, si
   return TCO_OK;
 }
 
+/* The beam-search branch of the same loop, do_sample = false
+ * (generation.rs:643-664 and 671-679): each row's log_softmax, penalty and
+ * typical warper only (the do_sample warpers are skipped), the joint
+ * beam-major scores, every flat index sorted by joint score descending
+ * (stable, so equal scores keep ascending flat order), truncated to n_keep,
+ * then sorted by score descending again (stable: the same order). */
+int tco_idx_beam_search_step(const tco_params* p, const float* logits, size_t batch, size_t nb, size_t V,
+                             const uint32_t* hist_off, const uint32_t* hist_ids, const double* beam_scores,
+                             size_t n_keep, uint32_t* cand_flat, double* cand_scores) {
+  if (p->variant != TCO_INDEXTTS) return TCO_EINVAL;
+  int st = check_params(p);
+  if (st != TCO_OK) return st;
+  tco_params q = *p;
+  q.temperature = 1.0;
+  q.top_k = 0;
+  q.top_p = 1.0;
+  const size_t n = nb * V;
+  float* x = (float*)malloc((V ? V : 1) * sizeof(float));
+  double* joint = (double*)malloc((n ? n : 1) * sizeof(double));
+  for (size_t bi = 0; bi < batch; bi++) {
+    for (size_t j = 0; j < nb; j++) {
+      const size_t r = bi * nb + j;
+      memcpy(x, logits + r * V, V * sizeof(float));
+      const uint32_t* ids = NULL;
+      size_t n_ids = 0;
+      if (hist_off && hist_ids) { ids = hist_ids + hist_off[r]; n_ids = hist_off[r + 1] - hist_off[r]; }
+      idx_process_row(&q, x, V, ids, n_ids, NULL);
+      for (size_t i = 0; i < V; i++) joint[j * V + i] = (double)x[i] + beam_scores[r];
+    }
+    /* order.sort_by(|&a, &x| joint[x].total_cmp(&joint[a])) is stable: the
+     * first n_keep of it are the n_keep best under (total order descending,
+     * flat ascending), taken here by repeated scans (n_keep is small) */
+    {
+      unsigned char* used = (unsigned char*)calloc(n ? n : 1, 1);
+      for (size_t d = 0; d < n_keep; d++) {
+        size_t best = (size_t)-1;
+        for (size_t f = 0; f < n; f++) {
+          if (used[f]) continue;
+          if (best == (size_t)-1 || tkey64(joint[f]) > tkey64(joint[best])) best = f;
+        }
+        if (best == (size_t)-1) { cand_flat[bi * n_keep + d] = 0; cand_scores[bi * n_keep + d] = 0.0; continue; }
+        used[best] = 1;
+        cand_flat[bi * n_keep + d] = (uint32_t)best;
+        cand_scores[bi * n_keep + d] = joint[best];
+      }
+      free(used);
+    }
+  }
+  free(joint); free(x);
+  return TCO_OK;
+}
+
 int tco_sample(const tco_params* p, const float* logits, size_t rows, size_t V,
                const uint32_t* hist_off, const uint32_t* hist_ids, const void* uniforms,
                uint32_t* out_ids, int32_t* out_status, uint32_t* out_flags,

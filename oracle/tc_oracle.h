@@ -122,6 +122,11 @@ int tco_idx_beam_step(const tco_params* p, const float* logits, size_t batch, si
                       const uint32_t* hist_off, const uint32_t* hist_ids, const double* beam_scores,
                       const double* uniforms, size_t n_draws, uint32_t* cand_flat, double* cand_scores,
                       int32_t* status);
+/* generation.rs:671-679 (do_sample = false): the n_keep best joint scores per
+ * element, descending, equal scores in ascending flat order. */
+int tco_idx_beam_search_step(const tco_params* p, const float* logits, size_t batch, size_t nb, size_t V,
+                             const uint32_t* hist_off, const uint32_t* hist_ids, const double* beam_scores,
+                             size_t n_keep, uint32_t* cand_flat, double* cand_scores);
 
 /* ---- cosyvoice3 (crates/cosyvoice3/src/llm.rs) ---- */
 uint32_t tco_cosy_nucleus(const float* probs, size_t V, float top_p, size_t top_k, float u0,

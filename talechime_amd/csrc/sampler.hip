@@ -3359,6 +3359,91 @@ __global__ void __launch_bounds__(64) k_beam_joint(BeamArgs b) {
   }
 }
 
+// The beam-search branch (do_sample = false, generation.rs:671-679): the
+// n_keep best joint scores of each element over its beams' kept lists (the
+// row pass keeps every id at or above its row's n_keep-th score, ties
+// included, so they hold the element's best n_keep), descending, equal
+// scores in ascending flat order (the reference's stable sort of the flat
+// indices).  One wave per element, n_keep rounds of a wave arg-max.
+__global__ void __launch_bounds__(64) k_beam_topn(BeamArgs b) {
+  __shared__ BeamLds B;
+  const int bi = blockIdx.x, lane = threadIdx.x, nb = b.nb, nk = b.n_draws;
+  int32_t rs = TC_OK;
+  uint32_t cnt = 0u;
+  double bonus = 0.0;
+  if (lane < nb) {
+    const int r = bi * nb + lane;
+    rs = b.row_status[r];
+    cnt = b.keep_count[r];
+    bonus = b.beam_scores[r];
+  }
+  // a row without a finite score (TC_ETOOFEW) adds nothing; the first other
+  // failing row gives the element its status
+  const uint64_t fm = __ballot(lane < nb && rs != TC_OK && rs != TC_ETOOFEW);
+  int32_t st = fm ? (int32_t)rl_u32((uint32_t)rs, __builtin_ctzll(fm)) : TC_OK;
+  uint32_t c = (lane < nb && rs == TC_OK) ? cnt : 0u;
+  if (__ballot(c > (uint32_t)kBeamCap) && st == TC_OK) st = TC_EUNSUPPORTED;
+  c = c > (uint32_t)kBeamCap ? 0u : c;
+  const uint32_t incl = dpp_scan_u32(c);
+  const uint32_t Lall = rl_u32(incl, kWave - 1);
+  if (Lall > (uint32_t)kJointCap && st == TC_OK) st = TC_EUNSUPPORTED;
+  const uint32_t L = st == TC_OK ? Lall : 0u;
+  if (lane < nb) B.off[lane] = incl - c;
+  __syncthreads();
+  for (int j = 0; j < nb && L; ++j) {
+    const int r = bi * nb + j;
+    const uint32_t o = B.off[j], cj = (j + 1 < nb ? B.off[j + 1] : L) - o;
+    const double bo = rl_f64(bonus, j);
+    for (uint32_t k = (uint32_t)lane; k < cj; k += 64u) {
+      B.s[o + k] = (double)b.keep_scores[(size_t)r * kBeamCap + k] + bo;
+      B.flat[o + k] = (uint32_t)j * (uint32_t)b.V + b.keep_ids[(size_t)r * kBeamCap + k];
+      B.gone[o + k] = 0;
+    }
+  }
+  __syncthreads();
+  const bool enough = L >= (uint32_t)nk;
+  for (int d = 0; d < nk && enough; ++d) {
+    // the best remaining entry: total order descending, then flat ascending
+    uint64_t bk = 0;
+    uint32_t bf = 0xffffffffu, bidx = 0xffffffffu;
+    for (uint32_t k = (uint32_t)lane; k < L; k += 64u) {
+      if (B.gone[k]) continue;
+      const uint64_t kk = tkey64(B.s[k]);
+      if (bidx == 0xffffffffu || kk > bk || (kk == bk && B.flat[k] < bf)) {
+        bk = kk;
+        bf = B.flat[k];
+        bidx = k;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t ok = __shfl_xor(bk, o);
+      const uint32_t of = __shfl_xor(bf, o), oi = __shfl_xor(bidx, o);
+      if (oi != 0xffffffffu && (bidx == 0xffffffffu || ok > bk || (ok == bk && of < bf))) {
+        bk = ok;
+        bf = of;
+        bidx = oi;
+      }
+    }
+    if (lane == 0) {
+      B.gone[bidx] = 1;
+      B.ps[d] = B.s[bidx];
+      B.pf[d] = bf;
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    double* cs = b.cand_scores + (size_t)bi * nk;
+    uint32_t* cf = b.cand_flat + (size_t)bi * nk;
+    for (int d = 0; d < nk; ++d) {
+      cs[d] = (st == TC_OK && enough) ? B.ps[d] : 0.0;
+      cf[d] = (st == TC_OK && enough) ? B.pf[d] : 0u;
+    }
+    b.out_status[bi] = st != TC_OK ? st : (enough ? TC_OK : TC_ETOOFEW);
+    if (b.out_flags) b.out_flags[bi] = 0u;
+  }
+}
+
 }  // namespace tc
 
 // ====================================================================== C ABI
@@ -3737,7 +3822,7 @@ static int beam_step_impl(int device, size_t max_vocab, void* ws, size_t ws_rows
                           size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
                           const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
                           size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
-                          uint32_t* d_out_flags, tc_stream stream) {
+                          uint32_t* d_out_flags, tc_stream stream, bool search = false) {
   const size_t rows = batch * num_beams;
   const BeamWs w = beam_ws(ws, ws_rows);
   tc_verify_out v{};
@@ -3750,6 +3835,14 @@ static int beam_step_impl(int device, size_t max_vocab, void* ws, size_t ws_rows
   v.d_norm = nullptr;
   tc_sample_params rp = *p;
   rp.d_mark_mask = nullptr;
+  if (search) {
+    // without sampling the row keeps log_softmax and the penalty only
+    // (generation.rs:653-662), and its n_keep best scores, ties included
+    rp.temperature = 1.0;
+    rp.top_p = 1.0;
+    rp.top_k = (uint32_t)n_draws;
+    rp.min_keep = 0;
+  }
   int rc = sample_impl(device, max_vocab, &rp, d_logits, dtype, rows, vocab, ld, d_hist_off, d_hist_ids, zero_u,
                        w.ids, w.status, w.flags, &v, w.keep_scores, stream);
   if (rc != TC_OK) return rc;
@@ -3768,7 +3861,10 @@ static int beam_step_impl(int device, size_t max_vocab, void* ws, size_t ws_rows
   b.cand_scores = d_cand_scores;
   b.out_status = d_out_status;
   b.out_flags = d_out_flags;
-  hipLaunchKernelGGL(tc::k_beam_joint, dim3((unsigned)batch), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), b);
+  if (search)
+    hipLaunchKernelGGL(tc::k_beam_topn, dim3((unsigned)batch), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), b);
+  else
+    hipLaunchKernelGGL(tc::k_beam_joint, dim3((unsigned)batch), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), b);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TC_OK : hip_fail(e, "tc_indextts_beam_step launch");
 }
@@ -3793,6 +3889,23 @@ static int beam_check(const char* fn, const tc_sample_params* p, const void* d_l
   return TC_OK;
 }
 
+// The context's beam workspace (allocated on its first beam step): R zero
+// uniforms, then the row-pass workspace of R rows.  The caller made the
+// context's device current.
+static int ctx_beam_ws(tc_ctx* ctx) {
+  if (ctx->d_beam) return TC_OK;
+  const size_t R = ctx->max_rows;
+  const size_t bytes = R * 8 + beam_ws_bytes(R);
+  hipError_t e = hipMalloc(&ctx->d_beam, bytes);
+  if (e != hipSuccess) {
+    ctx->d_beam = nullptr;
+    return fail(TC_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  }
+  e = hipMemset(ctx->d_beam, 0, bytes);
+  if (e != hipSuccess) return hip_fail(e, "hipMemset");
+  return TC_OK;
+}
+
 int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,
                           size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
                           const uint32_t* d_hist_ids, const double* d_beam_scores, const double* d_uniforms,
@@ -3805,22 +3918,38 @@ int tc_indextts_beam_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_
   const size_t rows = batch * num_beams;
   if (rows > ctx->max_rows) return fail(TC_EINVAL, "tc_indextts_beam_step: %zu rows > context max %zu", rows, ctx->max_rows);
   DeviceGuard g(ctx->device);
+  rc = ctx_beam_ws(ctx);
+  if (rc != TC_OK) return rc;
   const size_t R = ctx->max_rows;
-  if (!ctx->d_beam) {
-    const size_t bytes = R * 8 + beam_ws_bytes(R);
-    hipError_t e = hipMalloc(&ctx->d_beam, bytes);
-    if (e != hipSuccess) {
-      ctx->d_beam = nullptr;
-      return fail(TC_ENOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
-    }
-    e = hipMemset(ctx->d_beam, 0, bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMemset");
-  }
   const double* zero_u = static_cast<const double*>(ctx->d_beam);
   void* ws = static_cast<char*>(ctx->d_beam) + R * 8;
   return beam_step_impl(ctx->device, ctx->max_vocab, ws, R, zero_u, p, d_logits, dtype, batch, num_beams, vocab, ld,
                         d_hist_off, d_hist_ids, d_beam_scores, d_uniforms, n_draws, d_cand_flat, d_cand_scores,
                         d_out_status, d_out_flags, stream);
+}
+
+int tc_indextts_beam_search_step(tc_ctx* ctx, const tc_sample_params* p, const void* d_logits, int dtype,
+                                 size_t batch, size_t num_beams, size_t vocab, size_t ld, const uint32_t* d_hist_off,
+                                 const uint32_t* d_hist_ids, const double* d_beam_scores, size_t n_keep,
+                                 uint32_t* d_cand_flat, double* d_cand_scores, int32_t* d_out_status,
+                                 tc_stream stream) {
+  if (!ctx) return fail(TC_EINVAL, "tc_indextts_beam_search_step: ctx is NULL");
+  // the uniforms argument is not read in this mode: d_beam_scores stands in
+  int rc = beam_check("tc_indextts_beam_search_step", p, d_logits, batch, num_beams, vocab, d_beam_scores,
+                      d_beam_scores, n_keep, d_cand_flat, d_cand_scores, d_out_status);
+  if (rc != TC_OK || batch == 0) return rc;
+  const size_t rows = batch * num_beams;
+  if (rows > ctx->max_rows)
+    return fail(TC_EINVAL, "tc_indextts_beam_search_step: %zu rows > context max %zu", rows, ctx->max_rows);
+  DeviceGuard g(ctx->device);
+  rc = ctx_beam_ws(ctx);
+  if (rc != TC_OK) return rc;
+  const size_t R = ctx->max_rows;
+  const double* zero_u = static_cast<const double*>(ctx->d_beam);
+  void* ws = static_cast<char*>(ctx->d_beam) + R * 8;
+  return beam_step_impl(ctx->device, ctx->max_vocab, ws, R, zero_u, p, d_logits, dtype, batch, num_beams, vocab, ld,
+                        d_hist_off, d_hist_ids, d_beam_scores, nullptr, n_keep, d_cand_flat, d_cand_scores,
+                        d_out_status, nullptr, stream, true);
 }
 
 int tc_indextts_beam_step_noalloc(const tc_sample_params* p, const void* d_logits, int dtype, size_t batch,

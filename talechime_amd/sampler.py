@@ -190,6 +190,48 @@ class DeviceSampler:
         return out
 
 
+    def beam_search_step(self, params: SampleParams, logits: torch.Tensor, hist_off: torch.Tensor | None,
+                         hist_ids: torch.Tensor | None, beam_scores: torch.Tensor, num_beams: int,
+                         n_keep: int | None = None, *, stream: torch.cuda.Stream | None = None) -> BeamCandidates:
+        """The beam-search branch of the same loop (do_sample = false,
+        generation.rs:671-679): the n_keep best joint scores of each element
+        (log_softmax and the penalty only), descending.  ``n_keep`` defaults
+        to 2 * num_beams as in the reference."""
+        if params.variant != INDEXTTS:
+            raise ValueError("beam_search_step takes indextts rows")
+        if logits.dim() != 2 or logits.stride(1) != 1 or not logits.is_cuda:
+            raise ValueError("logits must be a 2-D GPU tensor with unit stride in the vocab dim")
+        dt = {torch.float32: F32, torch.bfloat16: BF16}.get(logits.dtype)
+        if dt is None:
+            raise ValueError(f"logits dtype {logits.dtype} (f32 or bf16 expected)")
+        rows, V = logits.shape
+        if num_beams < 1 or rows % num_beams:
+            raise ValueError("rows must be a multiple of num_beams")
+        batch = rows // num_beams
+        n_keep = 2 * num_beams if n_keep is None else n_keep
+        _need_cuda(beam_scores, torch.float64, "beam_scores")
+        if beam_scores.numel() < rows:
+            raise ValueError("beam_scores needs one score per row")
+        ho = hi = None
+        if hist_off is not None:
+            _need_cuda(hist_off, None, "hist_off")
+            _need_cuda(hist_ids, None, "hist_ids")
+            if hist_off.element_size() != 4 or hist_ids.element_size() != 4 or hist_off.numel() < rows + 1:
+                raise ValueError("histories: rows + 1 32-bit offsets and 32-bit ids")
+            ho, hi = hist_off.data_ptr(), hist_ids.data_ptr() if hist_ids.numel() else hist_off.data_ptr()
+        dev = logits.device
+        out = BeamCandidates(torch.empty(batch, n_keep, dtype=torch.int32, device=dev),
+                             torch.empty(batch, n_keep, dtype=torch.float64, device=dev),
+                             torch.empty(batch, dtype=torch.int32, device=dev),
+                             torch.zeros(batch, dtype=torch.int32, device=dev))
+        st = (stream or torch.cuda.current_stream(dev)).cuda_stream
+        check(load().tc_indextts_beam_search_step(self._ctx, C.byref(params), logits.data_ptr(), dt, batch,
+                                                  num_beams, V, logits.stride(0), ho, hi, beam_scores.data_ptr(),
+                                                  n_keep, out.flat.data_ptr(), out.scores.data_ptr(),
+                                                  out.status.data_ptr(), st))
+        return out
+
+
 @dataclass
 class BeamCandidates:
     flat: torch.Tensor    # [batch, n_draws] int32 (u32 bits): beam * V + id

@@ -189,3 +189,47 @@ def test_beam_step_bf16_rows(sampler):
          "status": r.status.cpu().numpy(), "flags": r.flags.cpu().numpy()}
     o = O.idx_beam_step(O.make_params(O.INDEXTTS, **_kw(penalty=1.0)), xf, None, None, bonus, nb, u, 6)
     _compare(g, o, "bf16")
+
+
+@pytest.mark.parametrize("first_step", [True, False])
+@pytest.mark.parametrize("batch_index", [0, 1])
+def test_beam_search_step_matches_oracle(sampler, first_step, batch_index):
+    # do_sample = false (generation.rs:671-679): the 6 best joint scores of
+    # each of 64 elements x 3 beams, bit for bit; the sampling warpers set in
+    # the parameters are not applied
+    from talechime_amd.sampler import make_params
+    bb = synth.make_beam_batch(W, 64, 3, first_step=first_step, batch_index=batch_index)
+    dho = torch.from_numpy(bb.hist_off.view(np.int32).copy()).cuda()
+    dhi = torch.from_numpy(bb.hist_ids.view(np.int32).copy()).cuda()
+    p = make_params(_lib.INDEXTTS, **_kw())
+    r = sampler.beam_search_step(p, torch.from_numpy(bb.logits).cuda(), dho, dhi,
+                                 torch.from_numpy(bb.beam_scores).cuda(), 3)
+    torch.cuda.synchronize()
+    o = O.idx_beam_search_step(O.make_params(O.INDEXTTS, **_kw()), bb.logits, bb.hist_off, bb.hist_ids,
+                               bb.beam_scores, 3, 6)
+    assert (r.status.cpu().numpy() == 0).all()
+    assert np.array_equal(r.flat.cpu().numpy().view(np.uint32), o["flat"])
+    assert np.array_equal(r.scores.cpu().numpy().view(np.int64), o["scores"].view(np.int64))
+
+
+def test_beam_search_step_ties_in_flat_order(sampler):
+    # two beams with equal rows, histories and beam scores: every joint score
+    # is tied across them and beam 0's flat index comes first
+    from talechime_amd.sampler import make_params
+    g = np.random.default_rng(3)
+    V = W.vocab
+    x = (g.standard_normal((3, V)) * 4).astype(np.float32)
+    x[1] = x[0]
+    hist = [g.integers(0, V, 200).astype(np.uint32)] * 2 + [g.integers(0, V, 200).astype(np.uint32)]
+    off = np.zeros(4, np.uint32)
+    off[1:] = np.cumsum([h.size for h in hist])
+    ids = np.concatenate(hist)
+    bonus = np.array([-1.5, -1.5, -40.0])
+    p = make_params(_lib.INDEXTTS, **_kw())
+    r = sampler.beam_search_step(p, torch.from_numpy(x).cuda(), torch.from_numpy(off.view(np.int32)).cuda(),
+                                 torch.from_numpy(ids.view(np.int32)).cuda(), torch.from_numpy(bonus).cuda(), 3)
+    torch.cuda.synchronize()
+    o = O.idx_beam_search_step(O.make_params(O.INDEXTTS, **_kw()), x, off, ids, bonus, 3, 6)
+    f = r.flat.cpu().numpy().view(np.uint32)[0]
+    assert np.array_equal(f, o["flat"][0])
+    assert [int(v) // V for v in f] == [0, 1] * 3

@@ -425,3 +425,52 @@ def test_moss_errors_and_greedy(oracle):
                              exclude_id=1)
     r = oracle.sample(prm, x, np.array([0, 0], np.uint32), np.zeros(0, np.uint32), np.array([0.99]))
     assert r["ids"][0] in (0, 2)
+
+
+# --------------------------------------------------------------------- indextts beam search (do_sample = false)
+def _processed(oracle, row, hist, pen):
+    r = oracle.idx_log_softmax(row)
+    return oracle.idx_penalty(r, hist, pen) if pen != 1.0 else r
+
+
+def test_indextts_beam_search_selects_best_joint_scores(oracle):
+    # generation.rs:671-679: every flat index sorted by joint score descending
+    # (a stable sort: equal scores in ascending flat order), truncated to
+    # n_keep.  Checked against numpy's stable argsort of the joint scores the
+    # oracle's own (pinned) processors give.
+    g = np.random.default_rng(9)
+    nb, V, n_keep = 3, 257, 6
+    x = (g.standard_normal((2 * nb, V)) * 3).astype(np.float32)
+    x[1] = x[0]                      # a beam equal to beam 0: every score tied across them
+    bonus = np.array([0.0, 0.0, -1e9, -0.5, -1.25, -3.0])
+    hist = [g.integers(0, V, 40).astype(np.uint32) for _ in range(2 * nb)]
+    hist[1] = hist[0]                # and the same history
+    off = np.zeros(2 * nb + 1, np.uint32)
+    off[1:] = np.cumsum([h.size for h in hist])
+    prm = oracle.make_params(oracle.INDEXTTS, temperature=0.7, top_k=5, top_p=0.5, penalty=1.7)
+    r = oracle.idx_beam_search_step(prm, x, off, np.concatenate(hist), bonus, nb, n_keep)
+    for bi in range(2):
+        joint = np.concatenate([_processed(oracle, x[bi * nb + j], hist[bi * nb + j], 1.7).astype(np.float64)
+                                + bonus[bi * nb + j] for j in range(nb)])
+        want = np.argsort(-joint, kind="stable")[:n_keep]
+        assert r["flat"][bi].tolist() == want.tolist()
+        assert r["scores"][bi].tolist() == joint[want].tolist()
+    # element 0: beams 0 and 1 tie everywhere, so each pair of candidates is
+    # (beam 0 id, beam 1 id) for the same id, beam 0 first
+    f = r["flat"][0]
+    assert [int(v) // V for v in f] == [0, 1] * (n_keep // 2)
+    assert all(int(f[i]) % V == int(f[i + 1]) % V for i in range(0, n_keep, 2))
+
+
+def test_indextts_beam_search_skips_the_sampling_warpers(oracle):
+    # temperature, top-k and top-p apply only when sampling (generation.rs:653-662):
+    # the joint scores are the log-probs with the penalty, whatever they are set to
+    g = np.random.default_rng(10)
+    V = 100
+    x = (g.standard_normal((1, V)) * 2).astype(np.float32)
+    a = oracle.idx_beam_search_step(oracle.make_params(oracle.INDEXTTS, temperature=0.3, top_k=2, top_p=0.1),
+                                    x, None, None, np.zeros(1), 1, 8)
+    b = oracle.idx_beam_search_step(oracle.make_params(oracle.INDEXTTS), x, None, None, np.zeros(1), 1, 8)
+    assert a["flat"].tolist() == b["flat"].tolist() and a["scores"].tolist() == b["scores"].tolist()
+    ls = oracle.idx_log_softmax(x[0]).astype(np.float64)
+    assert a["scores"][0].tolist() == np.sort(ls)[::-1][:8].tolist()
