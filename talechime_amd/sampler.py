@@ -1,7 +1,7 @@
 """Batched device sampler: torch tensors in, token ids out, through the C ABI.
 
-``DeviceSampler.sample`` is the one entry every host-side mirror
-(qwen / cosyvoice3 / indextts / moss) goes through.  Tensors must already be on
+``DeviceSampler.sample`` is the one entry the per-crate modules
+(qwen / cosyvoice3 / indextts / moss) go through.  Tensors must already be on
 the GPU; nothing is copied to the host unless the caller asks for it.
 """
 from __future__ import annotations
@@ -76,6 +76,7 @@ class DeviceSampler:
         self.device = torch.cuda.current_device() if device is None else int(device)
         self._ctx = C.c_void_p()
         check(L.tc_create(self.device, max_rows, max_vocab, C.byref(self._ctx)))
+        self.max_rows = max_rows
         self.max_vocab = max_vocab
 
     def close(self) -> None:

@@ -1,0 +1,154 @@
+"""The per-crate interfaces (talechime_amd.qwen / cosyvoice3 / indextts / moss)
+against the oracle: same tokens, and the host random streams advance exactly
+as the reference's do (greedy qwen steps draw nothing, cosyvoice3 draws a
+second uniform only when the repetition window fires, nano's LCG advances
+after the input checks)."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from talechime_amd import rng as R  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    return torch.device("cuda", 0)
+
+
+def test_qwen_sample_and_greedy_stream(dev):
+    from talechime_amd import qwen
+    g = np.random.default_rng(1)
+    x = (g.standard_normal((4, 3072)) * 3).astype(np.float32)
+    cfg = qwen.GenerationConfig(temperature=0.9, top_k=50, top_p=0.8)
+    ctx, ref = R.SamplingContext(42), R.SamplingContext(42)
+    for step in range(3):
+        ids = qwen.sample(torch.from_numpy(x + step).to(dev), cfg, ctx).cpu().numpy().view(np.uint32)
+        u = ref.draw(4)
+        o = O.sample(O.make_params(O.QWEN, temperature=0.9, top_k=50, top_p=0.8), x + step, None, None, u)
+        assert ids.tolist() == o["ids"].tolist()
+    # a greedy step consumes no uniform
+    greedy = qwen.GenerationConfig(temperature=0.005)
+    ids = qwen.sample(torch.from_numpy(x).to(dev), greedy, ctx).cpu().numpy().view(np.uint32)
+    assert ids.tolist() == np.argmax(x, axis=1).tolist()
+    assert ctx.next_u32() == ref.next_u32()
+
+
+def test_qwen_talker_step_chain(dev):
+    from talechime_amd import qwen
+    V, eos = 3072, 2150
+    g = np.random.default_rng(2)
+    cfg = qwen.GenerationConfig(temperature=0.9, top_k=50, top_p=0.8, repetition_penalty=1.05, eos_token_id=eos,
+                                min_new_tokens=2)
+    supp = qwen.build_suppression_mask(V, eos, dev)
+    pen = torch.zeros(V, dtype=torch.float32, device=dev)
+    ctx, ref = R.SamplingContext(7), R.SamplingContext(7)
+    ref_mask = np.zeros(V, np.float32)
+    sup_np = supp.cpu().numpy()
+    for step in range(5):
+        x = (g.standard_normal((1, V)) * 3).astype(np.float32)
+        x[0, eos] = 20.0  # EOS would win once it is allowed
+        tok = int(qwen.talker_step(torch.from_numpy(x).to(dev), cfg, ctx, pen, supp, step).cpu()[0])
+        p = O.make_params(O.QWEN, temperature=0.9, top_k=50, top_p=0.8, penalty=1.05, hist_mode=O.HIST_MASK,
+                          add_mask=sup_np, pen_mask=ref_mask.copy(), eos_id=eos if step < 2 else -1)
+        o = O.sample(p, x, None, None, ref.draw(1))
+        assert tok == int(o["ids"][0]), step
+        ref_mask[tok] = 1.0
+        assert np.array_equal(pen.cpu().numpy(), ref_mask)
+        if step < 2:
+            assert tok != eos
+
+
+def test_cosyvoice3_sample_advances_like_the_reference(dev):
+    from talechime_amd import cosyvoice3 as cv
+    V = 6564
+    g = np.random.default_rng(3)
+    cfg = cv.SamplingConfig()
+    rng, ref = R.StepRng(42), R.StepRng(42)
+    decoded, fired = [], 0
+    for step in range(12):
+        x = (g.standard_normal(V) * 3).astype(np.float32)
+        if decoded and step % 3 == 0:
+            x[decoded[-1]] += 12.0  # the last token again: the window fires
+        tok = cv.sample(torch.from_numpy(x).to(dev), decoded, cfg, rng, step < 2, speech_token_size=6561)
+        c = ref.clone()
+        u = np.array([c.next_f32(), c.next_f32()], np.float32)
+        hist = np.asarray(decoded, np.uint32)
+        o = O.sample(O.make_params(O.COSY_RAS, top_k=25, top_p=0.8, ras_win=10, ras_tau=0.1,
+                                   eos_id=6561 if step < 2 else -1),
+                     x[None, :], np.array([0, hist.size], np.uint32), hist, u)
+        assert tok == int(o["ids"][0]), step
+        ref.next_u32()
+        if o["flags"][0] & O.FLAG_RAS:
+            ref.next_u32()
+            fired += 1
+        assert (rng.state, rng.inc) == (ref.state, ref.inc), step
+        decoded.append(tok)
+    assert fired >= 1
+
+
+def test_indextts_rows_and_beam_steps(dev):
+    from talechime_amd import indextts as it
+    from talechime_amd import synth
+    w = synth.WORKLOADS["indextts-mel-256x8194"]
+    b = synth.make_batch(w, rows=16)
+    cfg = it.GenerateConfig()
+    hist = [b.hist_ids[b.hist_off[r]:b.hist_off[r + 1]].tolist() for r in range(16)]
+    ids = it.sample_rows(torch.from_numpy(b.logits).to(dev), hist, cfg, b.uniforms).cpu().numpy().view(np.uint32)
+    kw = dict(temperature=0.8, top_k=30, top_p=0.8, penalty=10.0, min_keep=2)
+    o = O.sample(O.make_params(O.INDEXTTS, **kw), b.logits_f32, b.hist_off, b.hist_ids, b.uniforms)
+    assert ids.tolist() == o["ids"].tolist()
+    bb = synth.make_beam_batch(w, 4, 3)
+    bh = [bb.hist_ids[bb.hist_off[r]:bb.hist_off[r + 1]].tolist() for r in range(12)]
+    c = it.beam_step(torch.from_numpy(bb.logits).to(dev), bh, bb.beam_scores, cfg, bb.uniforms)
+    ob = O.idx_beam_step(O.make_params(O.INDEXTTS, **kw), bb.logits, bb.hist_off, bb.hist_ids, bb.beam_scores, 3,
+                         bb.uniforms, 6)
+    near = (c.flags.cpu().numpy() & 16) != 0
+    assert np.array_equal(c.flat.cpu().numpy().view(np.uint32)[~near], ob["flat"][~near])
+    cs = it.beam_step(torch.from_numpy(bb.logits).to(dev), bh, bb.beam_scores, it.GenerateConfig(do_sample=False))
+    os_ = O.idx_beam_search_step(O.make_params(O.INDEXTTS, **kw), bb.logits, bb.hist_off, bb.hist_ids,
+                                 bb.beam_scores, 3, 6)
+    assert np.array_equal(cs.flat.cpu().numpy().view(np.uint32), os_["flat"])
+    with pytest.raises(NotImplementedError):
+        it.sample_rows(torch.from_numpy(b.logits).to(dev), hist, it.GenerateConfig(typical_sampling=True),
+                       b.uniforms)
+
+
+def test_moss_sample_and_nano_sampler(dev):
+    from talechime_amd import moss
+    g = np.random.default_rng(4)
+    V = 1027
+    prm = moss.Parameters(temperature=0.8, top_k=30, top_p=0.6, penalty=1.1)
+    for i in range(6):
+        x = (g.standard_normal(V) * 2).astype(np.float32)
+        hist = g.integers(0, V, 20).tolist()
+        gen, ref = np.random.default_rng(100 + i), np.random.default_rng(100 + i)
+        tok = moss.sample(torch.from_numpy(x).to(dev), hist, prm, 5, gen)
+        u = ref.random()
+        o = O.sample(O.make_params(O.MOSS, temperature=0.8, top_k=30, top_p=0.6, penalty=1.1, exclude_id=5),
+                     x[None, :], np.array([0, len(hist)], np.uint32), np.asarray(hist, np.uint32), np.array([u]))
+        assert tok == int(o["ids"][0])
+        assert gen.random() == ref.random()  # one draw each
+    # an error leaves the caller's stream where it was
+    bad = np.zeros(V, np.float32)
+    bad[3] = np.nan
+    gen, ref = np.random.default_rng(9), np.random.default_rng(9)
+    with pytest.raises(moss.MossError):
+        moss.sample(torch.from_numpy(bad).to(dev), [], prm, None, gen)
+    assert gen.random() == ref.random()
+    # nano: nano/sampling.rs:82-99 on the device, the LCG advancing once per draw
+    s = moss.Sampler(42)
+    x = torch.tensor([0.0, 1.0, 2.0, 3.0], device=dev)
+    assert s.sample(x, [], 1.0, 4, 1.0, 1.0) == 2
+    assert s.state == 1083814273  # 42 * 1664525 + 1013904223
+    with pytest.raises(moss.MossError):
+        s.sample(torch.tensor([0.0, float("nan")], device=dev), [], 1.0, 1, 1.0, 1.0)
+    assert s.state == 1083814273  # rejected before the draw
+    with pytest.raises(moss.MossError):
+        s.sample(torch.tensor([0.0, 1.0], device=dev), [5], 1.0, 1, 1.0, 2.0)
+    assert s.state == 1083814273
