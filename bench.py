@@ -52,6 +52,9 @@ def parse():
                          "and print the boundary-row counts")
     ap.add_argument("--beam", type=int, default=0, metavar="B",
                     help="time the indextts beam-sample step over B elements x 3 beams instead")
+    ap.add_argument("--head", type=int, default=0, metavar="R",
+                    help="time the indextts LM head (1280 -> 8194, bf16 weights) for R rows, alone and fused "
+                         "with the sampler, instead")
     ap.add_argument("--copy-calib", action="store_true",
                     help="after the timed region, copy 256 MiB three times (calibrates rocprofv3 byte counters)")
     return ap.parse_args()
@@ -291,6 +294,108 @@ def beam_bench(args):
     }), flush=True)
 
 
+def head_bench(args):
+    """The LM head before the sampler (tc_lm_head) for R rows of the indextts
+    mel_head (1280 -> 8194, bf16 weights, f32 bias), and the head fused with
+    the mel-code sampler (tc_head_sample).  A rotating pool of weight matrices
+    larger than twice the Infinity Cache keeps every launch reading HBM."""
+    import torch
+
+    from talechime_amd import synth
+    from talechime_amd.sampler import DeviceSampler, make_params
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    R, dim, vocab = args.head, 1280, 8194
+    wbytes = vocab * dim * 2
+    n_pool = max(2, int(np.ceil(args.pool_mb * 1e6 / wbytes)))
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    weights = [(torch.randn(vocab, dim, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(n_pool)]
+    bias = torch.randn(vocab, generator=g, device=dev) * 0.5
+    hidden = [torch.randn(R, dim, generator=g, device=dev) for _ in range(n_pool)]
+    logits = [torch.empty(R, vocab, device=dev) for _ in range(n_pool)]
+    w = synth.WORKLOADS["indextts-mel-256x8194"]
+    bt = synth.make_batch(w, rows=R)
+    ho = torch.from_numpy(bt.hist_off.view(np.int32).copy()).to(dev)
+    hi = torch.from_numpy(bt.hist_ids.view(np.int32).copy()).to(dev)
+    un = torch.from_numpy(bt.uniforms).to(dev)
+    sampler = DeviceSampler(0, max_rows=max(R, 8), max_vocab=vocab)
+    params = make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
+                         min_keep=w.min_keep)
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(step):
+        for j in range(n_pool):
+            step(j)
+        torch.cuda.synchronize()
+        full_replays, rest = divmod(max(1, args.steps), n_pool)
+
+        def capture(n):
+            if n == 0:
+                return None
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                for j in range(n):
+                    step(j)
+            return gr
+        full, part = capture(n_pool), capture(rest)
+        full.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(full_replays):
+            full.replay()
+        if part is not None:
+            part.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        n = full_replays * n_pool + rest
+        return e0.elapsed_time(e1) / n, n
+
+    ms_head, n = timed(lambda j: sampler.lm_head(hidden[j], weights[j], bias, out=logits[j]))
+    outs = [None] * n_pool
+
+    def fused(j):
+        outs[j] = sampler.head_sample(params, hidden[j], weights[j], bias, ho, hi, un, logits=logits[j])
+    ms_fused, _ = timed(fused)
+    st = outs[0].status.cpu().numpy()
+    if (st != 0).any():
+        print("bench.py: the fused head step returned a non-OK status", file=sys.stderr)
+        sys.exit(1)
+    step_bytes = wbytes + R * dim * 4 + vocab * 4 + R * vocab * 4
+    achieved = step_bytes / (ms_head * 1e-3) / 1e9
+    res = {
+        "metric": f"indextts mel_head GEMV (1280 -> 8194 bf16) steps/sec, {R} rows",
+        "value": round(1e3 / ms_head, 1), "unit": "steps/s", "n_gpus": 1, "steps": n, "warmup": n_pool,
+        "ms_per_step": round(ms_head, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 weights, f32 accumulation", "data": "synthetic (random weights and hidden states; rotating pool)",
+        "config": {"workload": f"indextts-mel-head-{R}x1280x8194", "rows": R, "dim": dim, "vocab": vocab,
+                   "pool_weights": n_pool},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": step_bytes},
+        "fused_head_and_sampler_us": round(ms_fused * 1e3, 3),
+    }
+    if not args.no_cpu:
+        # numpy's f32 matmul (its BLAS threads) and the oracle's sampler on the same rows
+        h0, w0, b0 = hidden[0].cpu().numpy(), weights[0].float().cpu().numpy(), bias.cpu().numpy()
+        from oracle import oracle as O
+        op = O.make_params(O.INDEXTTS, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p, penalty=w.penalty,
+                           min_keep=w.min_keep)
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds / 2:
+            lg = h0 @ w0.T + b0
+            O.sample(op, lg, bt.hist_off, bt.hist_ids, bt.uniforms)
+            done += 1
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": round(done / dt, 1), "unit": "steps/s", "cores": host_cpus()[0],
+                               "kind": "port", "sample": f"{done} head + sampler steps (numpy f32 matmul, the "
+                                                          f"oracle's sampler), {dt:.1f} s"}
+    sampler.close()
+    print(json.dumps(res), flush=True)
+
+
 def beam_cpu_baseline(w, bb, nb, seconds: float):
     """The oracle's beam step (C restatement of generation.rs:640-701) on this host."""
     from oracle import oracle as O
@@ -320,6 +425,8 @@ def main():
         return beam_bench(args)
     if args.parity:
         return parity_all(args.parity)
+    if args.head:
+        return head_bench(args)
     import torch
 
     from talechime_amd import synth

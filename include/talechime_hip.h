@@ -22,6 +22,8 @@
  *   tc_indextts_beam_step    crates/indextts/src/generation.rs:640-701, the joint scores
  *                            and sample_without_replacement of the beam-sample loop
  *   tc_indextts_beam_search_step  generation.rs:671-679, the same loop with do_sample false
+ *   tc_lm_head / tc_head_sample    the Linear before the sampler (generation.rs:632,
+ *                            code_predictor.rs:208-216), alone and with the sampler
  *   tc_sample (TC_MOSS)      crates/moss-tts/src/sampling.rs:22 `sample`
  *   tc_sample (TC_MOSS_NANO) crates/moss-tts/src/nano/sampling.rs:11 `Sampler::sample`
  *   tc_apply_repetition_penalty            sampling.rs:334
@@ -225,6 +227,34 @@ int tc_indextts_beam_step_noalloc(const tc_sample_params* params, const void* d_
                                   const double* d_beam_scores, const double* d_uniforms,
                                   size_t n_draws, uint32_t* d_cand_flat, double* d_cand_scores,
                                   int32_t* d_out_status, uint32_t* d_out_flags, tc_stream stream);
+
+/*
+ * The LM head that feeds the sampler: logits[r] = weight . hidden[r] + bias, the
+ * candle Linear of crates/indextts/src/generation.rs:632 (mel_head, 1280 -> 8194,
+ * with a bias, :981) and of the qwen3-tts code predictor's lm_heads
+ * (crates/qwen3-tts/src/models/code_predictor.rs:208-216, no bias).
+ *   d_hidden [rows, hidden_ld] f32; d_weight [vocab, dim] f32 or bf16 (tc_dtype),
+ *   16-byte aligned, rows of dim elements; d_bias [vocab] f32 or NULL;
+ *   d_logits [rows, logits_ld] f32.  dim a multiple of 8 (bf16) or 4 (f32), at most
+ *   4096 (bf16) or 2048 (f32).  f32 accumulation; the summation order is this
+ *   library's (the reference's matmul has its own), so the logits agree with an
+ *   exact product to within rounding, not bit for bit.
+ */
+int tc_lm_head(const float* d_hidden, size_t hidden_ld, const void* d_weight, int w_dtype, const float* d_bias,
+               size_t rows, size_t dim, size_t vocab, float* d_logits, size_t logits_ld, tc_stream stream);
+
+/*
+ * tc_lm_head then tc_sample on its logits, in one call on one stream: the head's
+ * output stays on the device (d_logits, [rows, vocab] f32, caller-owned) and the
+ * sampler reads it back from the cache.  Replaces the head + sample pair of one AR
+ * step (generation.rs:628-662; code_predictor.rs with sampling.rs:137).
+ * Arguments as tc_lm_head and tc_sample (no verification outputs).
+ */
+int tc_head_sample(tc_ctx* ctx, const tc_sample_params* params, const float* d_hidden, size_t hidden_ld,
+                   const void* d_weight, int w_dtype, const float* d_bias, size_t rows, size_t dim, size_t vocab,
+                   float* d_logits, const uint32_t* d_hist_off, const uint32_t* d_hist_ids,
+                   const void* d_uniforms, uint32_t* d_out_ids, int32_t* d_out_status, uint32_t* d_out_flags,
+                   tc_stream stream);
 
 /* qwen building blocks on f32 [rows, ld] (d_in may equal d_out).
  * tc_apply_repetition_penalty builds its [V] mask in the context's workspace. */

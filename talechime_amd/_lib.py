@@ -28,7 +28,7 @@ EXPORTS = (
     "tc_apply_repetition_penalty_with_mask", "tc_build_suppression_mask",
     "tc_apply_token_suppression_with_mask", "tc_update_penalty_mask", "tc_greedy_sample",
     "tc_last_error", "tc_abi_version", "tc_indextts_beam_step", "tc_indextts_beam_step_noalloc",
-    "tc_indextts_beam_search_step",
+    "tc_indextts_beam_search_step", "tc_lm_head", "tc_head_sample",
 )
 
 
@@ -106,6 +106,11 @@ def load(path: str = LIB_PATH):
     L.tc_indextts_beam_step.restype = C.c_int
     L.tc_indextts_beam_step.argtypes = [vp, C.POINTER(SampleParams), vp, C.c_int, sz, sz, sz, sz, vp, vp, vp, vp,
                                         sz, vp, vp, vp, vp, vp]
+    L.tc_lm_head.restype = C.c_int
+    L.tc_lm_head.argtypes = [vp, sz, vp, C.c_int, vp, sz, sz, sz, vp, sz, vp]
+    L.tc_head_sample.restype = C.c_int
+    L.tc_head_sample.argtypes = [vp, C.POINTER(SampleParams), vp, sz, vp, C.c_int, vp, sz, sz, sz, vp, vp, vp, vp,
+                                 vp, vp, vp, vp]
     L.tc_indextts_beam_search_step.restype = C.c_int
     L.tc_indextts_beam_search_step.argtypes = [vp, C.POINTER(SampleParams), vp, C.c_int, sz, sz, sz, sz, vp, vp,
                                                vp, sz, vp, vp, vp, vp]

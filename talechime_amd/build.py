@@ -76,7 +76,7 @@ def hipcc() -> str:
 
 
 def build_lib() -> str:
-    srcs = [os.path.join(CSRC, "sampler.hip")]
+    srcs = [os.path.join(CSRC, "sampler.hip"), os.path.join(CSRC, "lm_head.hip")]
     out_tmp = LIB + ".tmp"
     cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *srcs, "-o", out_tmp]
     subprocess.run(cmd, check=True)

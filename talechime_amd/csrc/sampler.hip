@@ -3472,6 +3472,14 @@ int fail(int code, const char* fmt, ...) {
 int hip_fail(hipError_t e, const char* what) {
   return fail(TC_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
+}  // namespace
+
+namespace tc {
+// The error slot of tc_last_error, for the library's other source files.
+int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace tc
+
+namespace {
 
 struct DeviceGuard {
   int prev = -1;

@@ -233,6 +233,66 @@ class DeviceSampler:
         return out
 
 
+    def lm_head(self, hidden: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+                out: torch.Tensor | None = None, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        """The Linear before the sampler (tc_lm_head): [rows, dim] f32 hidden
+        states, [vocab, dim] f32 or bf16 weights, optional [vocab] f32 bias;
+        returns [rows, vocab] f32 logits."""
+        h = hidden.reshape(-1, hidden.shape[-1])
+        if h.dtype != torch.float32 or h.stride(-1) != 1 or not h.is_cuda:
+            raise ValueError("hidden must be f32 on the GPU with unit stride")
+        if weight.dim() != 2 or not weight.is_contiguous() or not weight.is_cuda:
+            raise ValueError("weight must be a contiguous [vocab, dim] GPU tensor")
+        wdt = {torch.float32: F32, torch.bfloat16: BF16}.get(weight.dtype)
+        if wdt is None:
+            raise ValueError(f"weight dtype {weight.dtype} (f32 or bf16 expected)")
+        vocab, dim = weight.shape
+        if h.shape[1] != dim:
+            raise ValueError("hidden and weight disagree on dim")
+        if bias is not None:
+            _need_cuda(bias, torch.float32, "bias")
+        rows = h.shape[0]
+        if out is None:
+            out = torch.empty(rows, vocab, dtype=torch.float32, device=h.device)
+        st = (stream or torch.cuda.current_stream(h.device)).cuda_stream
+        check(load().tc_lm_head(h.data_ptr(), h.stride(0), weight.data_ptr(), wdt,
+                                bias.data_ptr() if bias is not None else None, rows, dim, vocab, out.data_ptr(),
+                                out.stride(0), st))
+        return out
+
+    def head_sample(self, params: SampleParams, hidden: torch.Tensor, weight: torch.Tensor,
+                    bias: torch.Tensor | None, hist_off: torch.Tensor | None, hist_ids: torch.Tensor | None,
+                    uniforms: torch.Tensor, *, logits: torch.Tensor | None = None,
+                    stream: torch.cuda.Stream | None = None) -> SampleResult:
+        """The head and the sampler in one call (tc_head_sample); ``logits``
+        is the [rows, vocab] f32 buffer the head writes (allocated when None)."""
+        h = hidden.reshape(-1, hidden.shape[-1])
+        vocab, dim = weight.shape
+        rows = h.shape[0]
+        if logits is None:
+            logits = torch.empty(rows, vocab, dtype=torch.float32, device=h.device)
+        if h.dtype != torch.float32 or h.stride(-1) != 1 or not weight.is_contiguous():
+            raise ValueError("hidden f32 with unit stride, weight contiguous")
+        wdt = {torch.float32: F32, torch.bfloat16: BF16}.get(weight.dtype)
+        if wdt is None:
+            raise ValueError(f"weight dtype {weight.dtype} (f32 or bf16 expected)")
+        need_u = torch.float64 if params.variant in (INDEXTTS, MOSS, MOSS_NANO) else torch.float32
+        _need_cuda(uniforms, need_u, "uniforms")
+        ho = hi = None
+        if hist_off is not None:
+            ho, hi = hist_off.data_ptr(), hist_ids.data_ptr() if hist_ids.numel() else hist_off.data_ptr()
+        dev = h.device
+        out = SampleResult(torch.empty(rows, dtype=torch.int32, device=dev),
+                           torch.empty(rows, dtype=torch.int32, device=dev),
+                           torch.empty(rows, dtype=torch.int32, device=dev))
+        st = (stream or torch.cuda.current_stream(dev)).cuda_stream
+        check(load().tc_head_sample(self._ctx, C.byref(params), h.data_ptr(), h.stride(0), weight.data_ptr(), wdt,
+                                    bias.data_ptr() if bias is not None else None, rows, dim, vocab,
+                                    logits.data_ptr(), ho, hi, uniforms.data_ptr(), out.ids.data_ptr(),
+                                    out.status.data_ptr(), out.flags.data_ptr(), st))
+        return out
+
+
 @dataclass
 class BeamCandidates:
     flat: torch.Tensor    # [batch, n_draws] int32 (u32 bits): beam * V + id
