@@ -30,6 +30,7 @@
 #include <stdio.h>
 
 #include <mutex>
+#include <type_traits>
 #include <string>
 
 #include "../../include/talechime_hip.h"
@@ -1456,6 +1457,9 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 //    it whose penalised logit reaches the bound, found as a second key
 //    threshold; at most kLargeCand), staged in vocabulary order a tile at a
 //    time.
+//  * Rows these passes do not decide (non-finite logits, a negative penalty,
+//    a K-th key more than 256 keys below the largest) take large_general,
+//    which streams the row from memory again and selects by logit.
 //  * A bitonic sort gives the reference's rank order (value descending, id
 //    ascending); top-k keeps every value >= the k-th (ties kept).
 //  * top-p: exact terms, the reference's sequential f32 sum in rank order and
@@ -1579,6 +1583,189 @@ __device__ __forceinline__ uint32_t half_mask(uint32_t m8, int j) {
 }
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+// The reference's logit of element e after the caller chain and temperature
+// (synthesis.rs:1238-1276, sampling.rs:175-184): the per-row penalty on ids in
+// the history (sn), the EOS id forced to -inf, then the multiply by f32(1/T).
+__device__ __forceinline__ float qlogit(const RowArgs& a, float x, bool sn, int e, int eos) {
+  float v = x;
+  if (a.do_pen && sn && e != eos) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
+  if (e == eos) v = -__builtin_inff();
+  if (a.do_temp) v = v * a.tmul + 0.0f;
+  return v;
+}
+
+// Candidates of the rows whose selection the register-tiled passes of
+// k_qwen_large do not decide: a non-finite logit, a negative penalty (the
+// penalised logit then falls as the bf16 value rises), a K-th largest key
+// more than 256 keys below the largest, or a K-th logit that overflowed to
+// -inf.  The row is streamed from memory again, in up to four passes:
+//  1. (non-finite rows) NaN and +inf after the caller chain, and the largest
+//     key outside the history over the ids whose logit is not NaN;
+//  2.-3. (K-th key not known) a radix select of the K-th largest key outside
+//     the history over its 16-bit distance below the largest, high byte
+//     first (runs of equal bins added at once), then the low byte;
+//  4. every id whose logit is not NaN and reaches the K-th key's logit (a
+//     superset of the reference's top-k survivors: the K-th logit over all
+//     ids is at least the K-th over those outside the history), staged in
+//     vocabulary order in S.cand and S.candv.
+// kmax and bK are the largest key outside the history and the K-th key's
+// distance below it when the caller knows them (bK 0xffffffff otherwise).
+// Returns the candidate count (the first kLargeCand staged), 0xffffffff when
+// a logit is +inf, and kLargeCand + 1 when fewer than K ids lie outside the
+// history.  NaN logits are left out and the row flagged TC_FLAG_NAN_ROW:
+// the reference's order for them at top-k is unspecified.
+__device__ __forceinline__ uint32_t large_general(const RowArgs& a, QLargeLds& S, const uint4* base, int nchunks,
+                                                 int shift, int eos, uint32_t kmax, uint32_t bK, bool nonfinite,
+                                                 uint32_t* row_flags) {
+  const int t = threadIdx.x, V = a.V, nwords = (V + 31) >> 5;
+  const int tile = kLargeU * (int)blockDim.x;
+  const uint32_t K = (uint32_t)a.K;
+  // every chunk once, thread t taking chunks tb + kLargeU * t + u of each tile
+  // (vocabulary order within the tile); the tile count is the same for all
+  auto walk = [&](auto&& body) __attribute__((always_inline)) {
+    for (int tb = 0; tb < nchunks; tb += tile) {
+      uint4 raw[kLargeU];
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(tb + kLargeU * t + u, nchunks - 1)];
+      body(raw, tb);
+    }
+  };
+  if (nonfinite) {
+    uint32_t nan = 0, pinf = 0, km = 0;
+    walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < kLargeU; ++u) {
+        const int q = tb + kLargeU * t + u;
+        if (q >= nchunks) break;
+        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int e = q * 8 - shift + h;
+          if (e < 0 || e >= V) continue;
+          const bool sn = (c.sn >> h) & 1u;
+          const float lv = qlogit(a, c.x[h], sn, e, eos);
+          if (__builtin_isnan(lv)) {
+            nan = 1u;
+            continue;
+          }
+          pinf |= lv == __builtin_inff() ? 1u : 0u;
+          if (!sn) km = max(km, ckey(c.x[h]) >> 16);
+        }
+      }
+    });
+    const bool any_nan = block_or_u(nan, S.s) != 0u;
+    pinf = block_or_u(pinf, S.s);
+    kmax = block_max_u(km, S.s);
+    if (any_nan) *row_flags |= TC_FLAG_NAN_ROW;
+    if (pinf) return 0xffffffffu;
+    bK = 0xffffffffu;
+  }
+  if (bK == 0xffffffffu) {
+    uint32_t hi = 0;
+    for (int lvl = 0; lvl < 2; ++lvl) {
+      if (t < 256) S.hist[t] = 0u;
+      __syncthreads();
+      walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+        uint32_t run_bin = 0xffffffffu, run_n = 0;
+#pragma unroll
+        for (int u = 0; u < kLargeU; ++u) {
+          const int q = tb + kLargeU * t + u;
+          if (q >= nchunks) break;
+          const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+          for (int h = 0; h < 8; ++h) {
+            const int e = q * 8 - shift + h;
+            // outside the history, inside the row, not NaN (such a logit is
+            // NaN exactly when its bf16 value is)
+            if (e < 0 || e >= V || ((c.sn >> h) & 1u) || __builtin_isnan(c.x[h])) continue;
+            const uint32_t dist = kmax - (ckey(c.x[h]) >> 16);
+            if (lvl == 1 && (dist >> 8) != hi) continue;
+            const uint32_t bin = lvl == 0 ? (dist >> 8) : (dist & 0xffu);
+            if (bin != run_bin) {
+              if (run_n) atomicAdd(&S.hist[run_bin], run_n);
+              run_bin = bin;
+              run_n = 0;
+            }
+            ++run_n;
+          }
+        }
+        if (run_n) atomicAdd(&S.hist[run_bin], run_n);
+      });
+      __syncthreads();
+      // the bin holding the K-th: the high level counts from the largest
+      // key, the low level what the higher bins left
+      const uint32_t need = lvl == 0 ? K : S.misc[1];
+      if (wave_id() == 0) {
+        const int l = lane_id();
+        const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
+        const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
+        uint32_t b = 0xffffffffu, before = 0;
+        if (ex + h0 >= need) { b = 4 * l; before = ex; }
+        else if (ex + h0 + h1 >= need) { b = 4 * l + 1; before = ex + h0; }
+        else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
+        else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
+        const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
+        if (l == 0) {
+          const int w = m ? __builtin_ctzll(m) : 0;
+          S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
+          S.misc[1] = m ? need - rl_u32(before, w) : 0u;
+        }
+      }
+      __syncthreads();
+      const uint32_t found = S.misc[0];
+      if (found == 0xffffffffu) return (uint32_t)kLargeCand + 1u;  // fewer than K ids outside the history
+      if (lvl == 0) hi = found;
+      else bK = (hi << 8) | found;
+      __syncthreads();
+    }
+  }
+  const uint32_t keyK = kmax - bK;
+  const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
+  const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
+  uint32_t n_c = 0;
+  walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+    uint32_t sel[kLargeU], cnt = 0;
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) {
+      sel[u] = 0u;
+      const int q = tb + kLargeU * t + u;
+      if (q < nchunks) {
+        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+          const int e = q * 8 - shift + h;
+          const float lv = qlogit(a, c.x[h], (c.sn >> h) & 1u, e, eos);
+          sel[u] |= (e >= 0 && e < V && !__builtin_isnan(lv) && lv >= thr) ? 1u << h : 0u;
+        }
+      }
+      cnt += (uint32_t)__builtin_popcount(sel[u]);
+    }
+    uint32_t tot;
+    uint32_t off = n_c + block_excl_scan(cnt, S.s, &tot);
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) {
+      const int c0 = (tb + kLargeU * t + u) * 8 - shift;
+      const uint32_t hb = sel[u] ? bits_at_fn(S.bits, nwords, c0) : 0u;
+      const uint32_t x = raw[u].x, y = raw[u].y, z = raw[u].z, w = raw[u].w;
+      for (uint32_t m = sel[u]; m; m &= m - 1u) {
+        const int h = __builtin_ctz(m);
+        const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
+        const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
+        const int e = c0 + h;
+        const float lv = qlogit(a, __uint_as_float(b), ((hb >> h) & 1u) != 0u || e == eos, e, eos);
+        if (off < (uint32_t)kLargeCand) {
+          const uint64_t kv = ((uint64_t)(~ckey(lv)) << 32) | (uint32_t)e;
+          S.cand[off] = kv;
+          S.candv[off] = kv;
+        }
+        ++off;
+      }
+    }
+    n_c += tot;
+  });
+  return n_c;
+}
+
 __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   __shared__ QLargeLds S;
   const int row = blockIdx.x, t = threadIdx.x, V = a.V;
@@ -1603,13 +1790,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   __syncthreads();
   // the reference's logit after the caller chain and temperature
   // (synthesis.rs:1238-1276, sampling.rs:175-184)
-  auto logit = [&](float x, bool sn, int e) {
-    float v = x;
-    if (a.do_pen && sn && e != eos) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
-    if (e == eos) v = -__builtin_inff();
-    if (a.do_temp) v = v * a.tmul + 0.0f;
-    return v;
-  };
+  auto logit = [&](float x, bool sn, int e) { return qlogit(a, x, sn, e, eos); };
   // Each streaming pass keeps kLargeU 16-byte loads in flight per thread (one
   // at a time leaves the pass bound by load latency, not by HBM).
   const int bd = (int)blockDim.x;
@@ -1729,287 +1910,152 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     no_verify(a, row);
     return;
   }
-  // Non-finite logits (rare): one more pass classifies them by their final
-  // logit.  A +inf logit survives top-k, makes every softmax weight NaN and
-  // sends the reference's CDF to index 0 (sampling.rs:302-328).  NaN logits
-  // take the reference's NaN path at top-k, whose order Rust leaves
-  // unspecified: they are left out here and the row is flagged; the largest
-  // key is then taken again without them.
-  bool row_nan = false;
-  uint32_t row_flags = 0;
-  if (bad) {
-    uint32_t pinf = 0, nan = 0, km = 0;
+  // Rows the streaming passes below do not decide -- non-finite logits, a
+  // negative penalty, a K-th key more than 256 keys below the largest, a K-th
+  // logit overflowing to -inf -- get their candidates from large_general,
+  // which streams the row again from memory; the common rows keep the row
+  // tiles in registers throughout.
+  const uint32_t K = (uint32_t)a.K;
+  uint32_t row_flags = 0, n_c = 0;
+  uint32_t bK = 0xffffffffu;
+  if (!bad) {
+    kmax = block_max_u(kmax, S.s);
+    // pass B: exact histogram of the 256 keys at and below the largest
+    // (two keys per 32-bit operation; a live key is at most kmax, so its
+    // 16-bit distance below kmax does not wrap)
+    const u16x2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
     tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
-#pragma unroll
+  #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
         if (q >= nchunks) break;
-        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
-#pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const int e = q * 8 - shift + h;
-          if (e < 0 || e >= V) continue;
-          const bool sn = (c.sn >> h) & 1u;
-          const float lv = logit(c.x[h], sn, e);
-          nan |= __builtin_isnan(lv) ? 1u : 0u;
-          pinf |= lv == __builtin_inff() ? 1u : 0u;
-          const uint32_t bb = f2u(c.x[h]);
-          if (!sn && e != eos && !((bb & 0x7f800000u) == 0x7f800000u && (bb & 0x007fffffu) != 0u))
-            km = max(km, ckey(c.x[h]) >> 16);
-        }
-      }
-    });
-    pinf = block_or_u(pinf, S.s);
-    row_nan = block_or_u(nan, S.s) != 0u;
-    row_flags = row_nan ? (uint32_t)TC_FLAG_NAN_ROW : 0u;
-    if (pinf) {
-      finish_row(a, row, 0u, TC_OK, row_flags);
-      no_verify(a, row);
-      return;
-    }
-    kmax = block_max_u(km, S.s);
-  } else {
-    kmax = block_max_u(kmax, S.s);
-  }
-  // the ids whose (widened bf16) logit is NaN, bit h of a chunk
-  auto nan8 = [&](const uint4& v, int c0) -> uint32_t {
-    uint32_t m = 0;
-    if (row_nan) {
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-      const uint32_t hb = bits_at_fn(S.bits, nwords, c0);
-#pragma unroll
-      for (int h = 0; h < 8; ++h) {
-        const int e = c0 + h;
-        const uint32_t b = (h & 1) ? (w[h >> 1] & 0xffff0000u) : (w[h >> 1] << 16);
-        const float lv = logit(__uint_as_float(b), ((hb >> h) & 1u) != 0u, e);
-        m |= (e >= 0 && e < V && __builtin_isnan(lv)) ? 1u << h : 0u;
-      }
-    }
-    return m;
-  };
-  // pass B: exact histogram of the 256 keys at and below the largest
-  // (two keys per 32-bit operation; a live key is at most kmax, so its
-  // 16-bit distance below kmax does not wrap)
-  const u16x2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
-  tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < kLargeU; ++u) {
-      const int q = tb + kLargeU * t + u;
-      if (q >= nchunks) break;
-      const int c0 = q * 8 - shift;  // in [-7, V)
-      const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-      uint32_t inm = 0xffu;
-      if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
-      if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
-      const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
-      const uint32_t live = inm & ~hb & ~em & ~nan8(raw[u], c0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, bkey16x2(u4_word(raw[u], j))));
-        if (((live >> (2 * j)) & 1u) && (d2 & 0xff00u) == 0u) atomicAdd(&S.hist[d2 & 0xffu], 1u);
-        if (((live >> (2 * j + 1)) & 1u) && (d2 >> 24) == 0u) atomicAdd(&S.hist[(d2 >> 16) & 0xffu], 1u);
-      }
-    }
-  });
-  __syncthreads();
-  const uint32_t K = (uint32_t)a.K;
-  if (wave_id() == 0) {
-    const int l = lane_id();
-    const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
-    const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
-    uint32_t b = 0xffffffffu;
-    if (ex + h0 >= K) b = 4 * l;
-    else if (ex + h0 + h1 >= K) b = 4 * l + 1;
-    else if (ex + h0 + h1 + h2 >= K) b = 4 * l + 2;
-    else if (inc >= K) b = 4 * l + 3;
-    const uint64_t m = __ballot(b != 0xffffffffu && ex < K);
-    if (l == 0) S.misc[0] = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;
-  }
-  __syncthreads();
-  uint32_t bK = S.misc[0];
-  if (bK == 0xffffffffu) {
-    // The K-th largest key lies more than 256 keys below the largest (peaked
-    // or shifted rows): a radix select over the full 16-bit distance, its
-    // high byte first (runs of equal bins added at once), then its low byte
-    // inside the chosen high-byte bin.
-    uint32_t lvl_hi = 0;
-    for (int lvl = 0; lvl < 2; ++lvl) {
-      if (t < 256) S.hist[t] = 0u;
-      __syncthreads();
-      tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
-        uint32_t run_bin = 0xffffffffu, run_n = 0;
-#pragma unroll
-        for (int u = 0; u < kLargeU; ++u) {
-          const int q = tb + kLargeU * t + u;
-          if (q >= nchunks) break;
-          const int c0 = q * 8 - shift;
-          const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-          uint32_t inm = 0xffu;
-          if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
-          if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
-          const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
-          const uint32_t live = inm & ~hb & ~em & ~nan8(raw[u], c0);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-              if (!((live >> (2 * j + hh)) & 1u)) continue;
-              const uint32_t dist = kmax - ((k2 >> (16 * hh)) & 0xffffu);
-              if (lvl == 1 && (dist >> 8) != lvl_hi) continue;
-              const uint32_t bin = lvl == 0 ? (dist >> 8) : (dist & 0xffu);
-              if (bin != run_bin) {
-                if (run_n) atomicAdd(&S.hist[run_bin], run_n);
-                run_bin = bin;
-                run_n = 0;
-              }
-              ++run_n;
-            }
-          }
-        }
-        if (run_n) atomicAdd(&S.hist[run_bin], run_n);
-      });
-      __syncthreads();
-      // the bin holding the K-th (the high level counts from the largest key;
-      // the low level counts what the higher bins left)
-      const uint32_t need = lvl == 0 ? K : S.misc[1];
-      if (wave_id() == 0) {
-        const int l = lane_id();
-        const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
-        const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
-        uint32_t b = 0xffffffffu, before = 0;
-        if (ex + h0 >= need) { b = 4 * l; before = ex; }
-        else if (ex + h0 + h1 >= need) { b = 4 * l + 1; before = ex + h0; }
-        else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
-        else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
-        const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
-        if (l == 0) {
-          const int w = m ? __builtin_ctzll(m) : 0;
-          S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
-          S.misc[1] = m ? need - rl_u32(before, w) : 0u;
-        }
-      }
-      __syncthreads();
-      if (S.misc[0] == 0xffffffffu) break;  // fewer than K ids outside the history
-      if (lvl == 0) lvl_hi = S.misc[0];
-      else bK = (lvl_hi << 8) | S.misc[0];
-      __syncthreads();
-    }
-    if (bK == 0xffffffffu) {
-      // fewer than K live ids (almost all in the history or excluded): every
-      // candidate must then be ranked, more than this kernel stages
-      finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
-      no_verify(a, row);
-      return;
-    }
-  }
-  const uint32_t keyK = kmax - bK;
-  const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
-  const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
-  // Penalised ids (in the history, not the EOS id) whose logit reaches thr.
-  // Their logit is a non-decreasing function of the bf16 value (a multiply by
-  // a positive factor, then by f32(1/T), each rounded), so they are the ids
-  // whose key reaches keyP, the smallest finite key whose penalised logit
-  // reaches thr (0xff80, above every finite key, when none does).  Both zeros
-  // share key 0x8000 and both give a logit of zero.  Every thread finds keyP
-  // by the same bisection over the finite keys [0x0080, 0xff7f].
-  // A negative penalty makes the penalised logit non-increasing in the bf16
-  // value: then keyP is the largest finite key whose penalised logit reaches
-  // thr, the ids at or below it qualify, and pass C compares the complemented
-  // keys of those ids (0xffff - key) against 0xffff - keyP.
-  const bool rev = a.do_pen && a.pen_f < 0.0f;
-  auto pen_logit = [&](uint32_t key) {  // logit() of a penalised id that is not EOS
-    const uint32_t b = (key & 0x8000u) ? (key & 0x7fffu) : (~key & 0xffffu);
-    const float x = __uint_as_float(b << 16);
-    float v = x * (x > 0.0f ? a.inv_pen : a.pen_f);
-    if (a.do_temp) v = v * a.tmul + 0.0f;
-    return v;
-  };
-  uint32_t keyP = 0xff80u;
-  if (a.do_pen && !rev) {
-    uint32_t lo = 0x0080u, hi = 0xff80u;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi) >> 1;
-      if (pen_logit(mid) >= thr) hi = mid;
-      else lo = mid + 1u;
-    }
-    keyP = lo;
-  } else if (rev) {
-    uint32_t lo = 0x0080u, hi = 0xff7fu;
-    while (lo < hi) {
-      const uint32_t mid = (lo + hi + 1u) >> 1;
-      if (pen_logit(mid) >= thr) lo = mid;
-      else hi = mid - 1u;
-    }
-    // complemented threshold; 0xffff (no finite complemented key reaches it)
-    // when no penalised logit reaches thr
-    keyP = pen_logit(lo) >= thr ? (0xffffu - lo) : 0xffffu;
-  }
-  // pass C: candidates in vocabulary order, a tile at a time.  Live ids are
-  // selected by key (two per instruction), penalised ones by the bitmap
-  // above.
-  uint32_t n_c = 0;
-  int parity = 0;
-  const uint32_t kK32 = keyK * 0x00010001u, kP32 = keyP * 0x00010001u;  // the thresholds in both halves
-  tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
-    uint64_t sel = 0, pens = 0;  // bit 8u + h
-#pragma unroll
-    for (int u = 0; u < kLargeU; ++u) {
-      const int q = tb + kLargeU * t + u;
-      if (q < nchunks) {
         const int c0 = q * 8 - shift;  // in [-7, V)
         const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
         uint32_t inm = 0xffu;
         if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
         if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
         const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
-        const uint32_t nm = nan8(raw[u], c0);
-        const uint32_t live = inm & ~hb & ~em & ~nm, pen = inm & hb & ~em & ~nm;
-        uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
-#pragma unroll
+        const uint32_t live = inm & ~hb & ~em;
+  #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t k2 = bkey16x2(u4_word(raw[u], j)) ^ (rev ? half_mask(pen, j) : 0u);
-          const uint32_t th2 = kP32 ^ ((kK32 ^ kP32) & half_mask(live, j));
-          const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2),
-                                                                                     __builtin_bit_cast(u16x2, th2)));
-          const uint32_t d = m2 ^ k2;  // 0 in a half where the key reaches its threshold
-          const uint32_t nz = (((d & 0x7fff7fffu) + 0x7fff7fffu) | d) & 0x80008000u;
-          ge |= (((~nz >> 15) & 1u) | ((~nz >> 30) & 2u)) << (2 * j);
+          const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, bkey16x2(u4_word(raw[u], j))));
+          if (((live >> (2 * j)) & 1u) && (d2 & 0xff00u) == 0u) atomicAdd(&S.hist[d2 & 0xffu], 1u);
+          if (((live >> (2 * j + 1)) & 1u) && (d2 >> 24) == 0u) atomicAdd(&S.hist[(d2 >> 16) & 0xffu], 1u);
         }
-        sel |= (uint64_t)((live | pen) & ge) << (8 * u);
-        pens |= (uint64_t)pen << (8 * u);
       }
-    }
-    const uint32_t cnt = (uint32_t)__popcll(sel);
-    const uint32_t ci = dpp_scan_u32(cnt);
-    if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
+    });
     __syncthreads();
-    uint32_t off, ntile;
-    wave_table_u32(S.wtot[parity], &off, &ntile);
-    off += n_c + ci - cnt;
-    if (sel && n_c + ntile <= (uint32_t)kLargeCand) {
-      // the set bits only (a few per lane); the chunk index stays static so
-      // that the chunk registers are never indexed at run time
-#pragma unroll
+    if (wave_id() == 0) {
+      const int l = lane_id();
+      const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
+      const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
+      uint32_t b = 0xffffffffu;
+      if (ex + h0 >= K) b = 4 * l;
+      else if (ex + h0 + h1 >= K) b = 4 * l + 1;
+      else if (ex + h0 + h1 + h2 >= K) b = 4 * l + 2;
+      else if (inc >= K) b = 4 * l + 3;
+      const uint64_t m = __ballot(b != 0xffffffffu && ex < K);
+      if (l == 0) S.misc[0] = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;
+    }
+    __syncthreads();
+    bK = S.misc[0];
+  }
+  const uint32_t keyK = kmax - bK;
+  const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
+  const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
+  if (bad || bK == 0xffffffffu || (a.do_pen && a.pen_f < 0.0f) || thr == -__builtin_inff()) {
+    n_c = large_general(a, S, base, nchunks, shift, eos, kmax, bad ? 0xffffffffu : bK, bad != 0u, &row_flags);
+    if (n_c == 0xffffffffu) {  // a +inf logit: the reference's CDF is NaN -> index 0
+      finish_row(a, row, 0u, TC_OK, row_flags);
+      no_verify(a, row);
+      return;
+    }
+  } else {
+    // Penalised ids (in the history, not the EOS id) whose logit reaches thr.
+    // Their logit is a non-decreasing function of the bf16 value (a multiply by
+    // a positive factor, then by f32(1/T), each rounded), so they are the ids
+    // whose key reaches keyP, the smallest finite key whose penalised logit
+    // reaches thr (0xff80, above every finite key, when none does).  Both zeros
+    // share key 0x8000 and both give a logit of zero.  Every thread finds keyP
+    // by the same bisection over the finite keys [0x0080, 0xff7f].
+    uint32_t keyP = 0xff80u;
+    if (a.do_pen) {
+      uint32_t lo = 0x0080u, hi = 0xff80u;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        const uint32_t b = (mid & 0x8000u) ? (mid & 0x7fffu) : (~mid & 0xffffu);
+        const float x = __uint_as_float(b << 16);
+        float v = x * (x > 0.0f ? a.inv_pen : a.pen_f);  // logit() for a penalised id that is not EOS
+        if (a.do_temp) v = v * a.tmul + 0.0f;
+        if (v >= thr) hi = mid;
+        else lo = mid + 1u;
+      }
+      keyP = lo;
+    }
+    // pass C: candidates in vocabulary order, a tile at a time.  Live ids are
+    // selected by key (two per instruction), penalised ones by the bitmap
+    // above.
+    int parity = 0;
+    const uint32_t kK32 = keyK * 0x00010001u, kP32 = keyP * 0x00010001u;  // the thresholds in both halves
+    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+      uint64_t sel = 0, pens = 0;  // bit 8u + h
+  #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
-        const uint32_t x = raw[u].x, y = raw[u].y, z = raw[u].z, w = raw[u].w;
-        const uint32_t pu = (uint32_t)(pens >> (8 * u));
-        for (uint32_t m = (uint32_t)(sel >> (8 * u)) & 0xffu; m; m &= m - 1u) {
-          const int h = __builtin_ctz(m);
-          const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
-          const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
-          const int e = (tb + kLargeU * t + u) * 8 - shift + h;
-          const float vv = logit(__uint_as_float(b), ((pu >> h) & 1u) != 0u, e);
-          const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
-          S.cand[off] = kv;
-          S.candv[off] = kv;
-          ++off;
+        const int q = tb + kLargeU * t + u;
+        if (q < nchunks) {
+          const int c0 = q * 8 - shift;  // in [-7, V)
+          const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
+          uint32_t inm = 0xffu;
+          if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+          if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+          const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+          const uint32_t live = inm & ~hb & ~em, pen = inm & hb & ~em;
+          uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
+            const uint32_t th2 = kP32 ^ ((kK32 ^ kP32) & half_mask(live, j));
+            const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2),
+                                                                                       __builtin_bit_cast(u16x2, th2)));
+            const uint32_t d = m2 ^ k2;  // 0 in a half where the key reaches its threshold
+            const uint32_t nz = (((d & 0x7fff7fffu) + 0x7fff7fffu) | d) & 0x80008000u;
+            ge |= (((~nz >> 15) & 1u) | ((~nz >> 30) & 2u)) << (2 * j);
+          }
+          sel |= (uint64_t)((live | pen) & ge) << (8 * u);
+          pens |= (uint64_t)pen << (8 * u);
         }
       }
-    }
-    n_c += ntile;
-    parity ^= 1;
-  });
+      const uint32_t cnt = (uint32_t)__popcll(sel);
+      const uint32_t ci = dpp_scan_u32(cnt);
+      if (lane_id() == kWave - 1) S.wtot[parity][wave_id()] = ci;
+      __syncthreads();
+      uint32_t off, ntile;
+      wave_table_u32(S.wtot[parity], &off, &ntile);
+      off += n_c + ci - cnt;
+      if (sel && n_c + ntile <= (uint32_t)kLargeCand) {
+        // the set bits only (a few per lane); the chunk index stays static so
+        // that the chunk registers are never indexed at run time
+  #pragma unroll
+        for (int u = 0; u < kLargeU; ++u) {
+          const uint32_t x = raw[u].x, y = raw[u].y, z = raw[u].z, w = raw[u].w;
+          const uint32_t pu = (uint32_t)(pens >> (8 * u));
+          for (uint32_t m = (uint32_t)(sel >> (8 * u)) & 0xffu; m; m &= m - 1u) {
+            const int h = __builtin_ctz(m);
+            const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
+            const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
+            const int e = (tb + kLargeU * t + u) * 8 - shift + h;
+            const float vv = logit(__uint_as_float(b), ((pu >> h) & 1u) != 0u, e);
+            const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
+            S.cand[off] = kv;
+            S.candv[off] = kv;
+            ++off;
+          }
+        }
+      }
+      n_c += ntile;
+      parity ^= 1;
+    });
+  }
   __syncthreads();
   if (n_c > (uint32_t)kLargeCand) {
     finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
@@ -2027,6 +2073,11 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   for (int j = t; j < (int)n_c; j += blockDim.x) ns_part += (uint32_t)(S.cand[j] >> 32) <= kth_hi ? 1u : 0u;
   const uint32_t ns = block_sum_u(ns_part, S.s);
   const float vmax = val_of(S.cand[0]);
+  if (vmax == __builtin_inff()) {  // a finite value overflowing to +inf: as above
+    finish_row(a, row, 0u, TC_OK, row_flags);
+    no_verify(a, row);
+    return;
+  }
   uint32_t flags = row_flags, cut = ns;
   if (a.do_topp) {
     // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential

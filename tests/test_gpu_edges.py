@@ -742,3 +742,26 @@ def test_qwen_large_vocab_infinities(sampler):
     assert g["ids"][3] == 0 and o["ids"][3] == 0
     tie = (o["flags"] & 1) != 0
     same(g, o, rows=[r for r in (1, 2) if not tie[r]])
+
+
+def test_qwen_large_vocab_overflow(sampler):
+    # finite bf16 logits that the temperature or the penalty carry past the
+    # f32 range: a +inf logit sends the CDF to index 0 as a +inf input does;
+    # a K-th logit of -inf keeps every id (each is >= -inf), more survivors
+    # than the kernel stages, so the row reports TC_EUNSUPPORTED
+    V = 151936
+    g_ = np.random.default_rng(79)
+    x = (g_.standard_normal((4, V)) * 3).astype(np.float32)
+    x[0, 777] = np.float32(3.0e38)          # x 2 (temperature 0.5) -> +inf
+    x[1, 888] = np.float32(3.0e38)          # in the history: x 1/0.6 -> +inf
+    x[2, :] = np.float32(-3.0e38)           # -> -inf everywhere but 30 ids
+    x[2, g_.integers(0, V, 30)] = g_.standard_normal(30).astype(np.float32)
+    hist = [[1], [888], [3], [4]]
+    u = g_.random(4)
+    g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, temperature=0.5, top_k=50, top_p=0.9, penalty=0.6)
+    assert g["status"][0] == 0 and g["ids"][0] == 0 and o["ids"][0] == 0
+    assert g["status"][1] == 0 and g["ids"][1] == 0 and o["ids"][1] == 0
+    assert g["status"][2] == _lib.TC_EUNSUPPORTED
+    assert g["status"][3] == 0
+    tie = (o["flags"] & 1) != 0
+    same(g, o, rows=[r for r in (3,) if not tie[r]])
