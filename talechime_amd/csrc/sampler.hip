@@ -1473,6 +1473,7 @@ constexpr int kLargeR = 3;  // tiles of kLargeU * blockDim chunks kept in regist
 constexpr int kLargePer = kLargeCand / kLargeThreads;  // candidate slots per thread
 constexpr int kLargeVocab = 262144;
 constexpr int kLargeWords = kLargeVocab / 32;
+static_assert(kLargeCand == 2048 && kLargeThreads == 1024, "block_sort2048 sorts 2048 keys over 1024 threads");
 
 struct QLargeLds {
   uint4 ltile[kLargeU * kLargeThreads];  // the row's tile kLargeR (chunk kLargeU * t + u at u * blockDim + t)
@@ -2062,10 +2063,12 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     no_verify(a, row);
     return;
   }
-  const int n_pad = next_pow2((int)n_c < 2 ? 2 : (int)n_c);
+  // rank order: more than 256 candidates sort as 2048 keys in registers
+  const int n_pad = n_c > 256u ? kLargeCand : next_pow2((int)n_c < 2 ? 2 : (int)n_c);
   for (int j = (int)n_c + t; j < n_pad; j += blockDim.x) S.cand[j] = ~0ull;
   __syncthreads();
-  block_bitonic_sort(S.cand, n_pad);
+  if (n_pad == kLargeCand) block_sort2048(S.cand);
+  else block_bitonic_sort(S.cand, n_pad);
   // top-k (sampling.rs:224-249): every value >= the K-th largest
   const uint32_t kth_hi = (uint32_t)(S.cand[K - 1] >> 32);  // ~ckey of the K-th value
   auto val_of = [](uint64_t kv) { return untkey(~(uint32_t)(kv >> 32)); };

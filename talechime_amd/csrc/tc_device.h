@@ -475,6 +475,73 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
   uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
   return ((uint64_t)hi << 32) | lo;
 }
+
+// ---------------------------------------------------------------- 2048-key sort
+// One compare-exchange of the bitonic network against lane t ^ d: the lower
+// position keeps the minimum when the run ascends.
+__device__ __forceinline__ uint64_t bitonic_lane(uint64_t x, int d, bool lower, bool up) {
+  const uint64_t y = shfl_xor_u64(x, d);
+  const uint64_t mn = x < y ? x : y, mx = x < y ? y : x;
+  return lower == up ? mn : mx;
+}
+__device__ __forceinline__ void bitonic_pair(uint64_t& x0, uint64_t& x1, bool up) {
+  const uint64_t lo = x0 < x1 ? x0 : x1, hi = x0 < x1 ? x1 : x0;
+  x0 = up ? lo : hi;
+  x1 = up ? hi : lo;
+}
+// LDS slot of position e in the transposition buffer: bits 8-9 folded into
+// bits 3-4, so that the column reads (positions c + 256 s) of a wave fall in
+// distinct bank pairs two lanes at a time.
+__device__ __forceinline__ int sort_slot(int e) { return e ^ (((e >> 8) & 3) << 3); }
+
+// Ascending sort of the 2048 keys at a (LDS) by a workgroup of exactly 1024
+// threads.  Thread t keeps positions 2t and 2t + 1 in registers; the network's
+// stages of stride 64 and below pair lanes of one wave (lane exchanges, no
+// barrier).  For merges of 256 keys and up, the stages of stride 128 and above
+// run in a transposed layout -- thread t holds positions c + 128 (2s) and
+// c + 128 (2s + 1), c = t / 8, s = t % 8 -- in which those partners are again
+// lanes of one wave; each switch of layout is one LDS round trip with one
+// barrier (each slot is read and later written by one thread only).  The
+// sorted keys are back at a, in order, when the call returns.
+__device__ __forceinline__ void block_sort2048(uint64_t* a) {
+  const int t = threadIdx.x, c = t >> 3, s = t & 7;
+  uint64_t x0 = a[2 * t], x1 = a[2 * t + 1];
+  __syncthreads();  // every key read before the buffer is reused
+  for (int k = 2, q = -6; k <= 2048; k <<= 1, ++q) {  // k = 128 * 2^q
+    if (k >= 256) {
+      a[sort_slot(2 * t)] = x0;
+      a[sort_slot(2 * t + 1)] = x1;
+      __syncthreads();
+      x0 = a[sort_slot(c + 256 * s)];
+      x1 = a[sort_slot(c + 256 * s + 128)];
+      const bool up = ((s >> (q - 1)) & 1) == 0;
+      for (int j = k >> 1; j >= 256; j >>= 1) {
+        const int d = j >> 8;
+        const bool lower = (s & d) == 0;
+        x0 = bitonic_lane(x0, d, lower, up);
+        x1 = bitonic_lane(x1, d, lower, up);
+      }
+      bitonic_pair(x0, x1, up);  // stride 128
+      a[sort_slot(c + 256 * s)] = x0;
+      a[sort_slot(c + 256 * s + 128)] = x1;
+      __syncthreads();
+      x0 = a[sort_slot(2 * t)];
+      x1 = a[sort_slot(2 * t + 1)];
+    }
+    const bool up = ((2 * t) & k) == 0;
+    for (int j = (k >> 1) < 64 ? (k >> 1) : 64; j >= 2; j >>= 1) {
+      const int d = j >> 1;
+      const bool lower = (t & d) == 0;
+      x0 = bitonic_lane(x0, d, lower, up);
+      x1 = bitonic_lane(x1, d, lower, up);
+    }
+    bitonic_pair(x0, x1, up);  // stride 1
+  }
+  __syncthreads();  // the last transposed reads done before the ordered writes
+  a[2 * t] = x0;
+  a[2 * t + 1] = x1;
+  __syncthreads();
+}
 // __builtin_amdgcn_readlane returns a signed int: go through uint32_t before
 // widening so the low word is not sign-extended.
 __device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
