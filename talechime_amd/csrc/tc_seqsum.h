@@ -68,18 +68,24 @@ __device__ __forceinline__ bool grid_round(float a, int g, int* r) {
 }
 
 // Index-selected read and write of a register array without dynamic
-// indexing (which would move the array to scratch memory).
+// indexing (which would move the array to scratch memory).  Masks on the bit
+// patterns rather than selects: a chain of selects between array elements
+// can be folded into one load from a computed address, which forces the
+// whole array into scratch for every path of the kernel.
 template <int ITEMS>
 __device__ __forceinline__ float pick_item(const float (&v)[ITEMS], int i) {
-  float r = v[0];
+  uint32_t r = 0;
 #pragma unroll
-  for (int j = 1; j < ITEMS; ++j) r = (i == j) ? v[j] : r;
-  return r;
+  for (int j = 0; j < ITEMS; ++j) r |= f2u(v[j]) & (0u - (uint32_t)(i == j));
+  return u2f(r);
 }
 template <int ITEMS>
 __device__ __forceinline__ void put_item(float (&v)[ITEMS], int i, float x) {
 #pragma unroll
-  for (int j = 0; j < ITEMS; ++j) v[j] = (i == j) ? x : v[j];
+  for (int j = 0; j < ITEMS; ++j) {
+    const uint32_t m = 0u - (uint32_t)(i == j);
+    v[j] = u2f((f2u(v[j]) & ~m) | (f2u(x) & m));
+  }
 }
 
 // Binade test and grid rounding of one element: returns 0 = safe (r set),
