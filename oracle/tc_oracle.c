@@ -17,14 +17,17 @@
  * breaks such ties by ascending vocabulary id and raises TCO_FLAG_TIE_CUT on
  * every row where the tie order could change the result.
  *
- * Pinning (tests/test_oracle_kats.py, tests/test_oracle_crosscheck.py): the
- * RNGs by their integer closed forms and the reference's constants; qwen,
- * indextts, cosyvoice3 and moss-nano by every vector of the reference's own
- * unit tests for these functions.  Parity unpinned:
+ * Pinning (tests/test_oracle_kats.py, tests/test_oracle_moss.py,
+ * tests/test_oracle_crosscheck.py): the RNGs by their integer closed forms and
+ * the reference's constants; qwen, indextts, cosyvoice3 and moss-nano by every
+ * vector of the reference's own unit tests for these functions; row_moss
+ * (moss-tts/src/sampling.rs:22-85), which has reference vectors only for its
+ * errors and greedy path, by what the mathematics fixes (rows of equal logits
+ * with exact weights and shares, rank-order CDFs, a brute force over a grid of
+ * uniforms against inverse-CDF intervals computed in double); the beam-search
+ * step by a stable argsort of the joint scores.  Parity unpinned:
  *   - the candle softmax summation order and the `Tensor / f64` lowering
- *     listed above (no reference test fixes them beyond dyadic rows);
- *   - row_moss (moss-tts/src/sampling.rs:22-85) beyond its error statuses and
- *     greedy path: checked only against the independent Python restatement.
+ *     listed above (no reference test fixes them beyond dyadic rows).
  */
 #define _GNU_SOURCE
 #include "tc_oracle.h"
