@@ -44,7 +44,7 @@
 extern "C" {
 #endif
 
-#define TC_ABI_VERSION 2
+#define TC_ABI_VERSION 3
 
 typedef struct tc_ctx tc_ctx;
 typedef void* tc_stream; /* a hipStream_t */
@@ -91,9 +91,10 @@ enum tc_flag {
                             uniform was used (the reference's StepRng advanced twice) */
   TC_FLAG_GREEDY = 4u,   /* qwen: temperature < 0.01, argmax, no uniform used */
   TC_FLAG_NAN_ROW = 8u,  /* qwen: NaN met at top-k (reference order unspecified) */
-  TC_FLAG_NEAR_TIE = 16u, /* indextts: a top-p or draw decision lay within the f64 exp
-                            error of the reference's libm (about 2^-46 relative); the
-                            id follows this library's exp */
+  TC_FLAG_NEAR_TIE = 16u, /* indextts: a top-p, draw or typical-warper decision lay
+                            within the error of this library's f64 exp and sums
+                            against the reference's (about 2^-46 relative); the id
+                            follows this library's arithmetic */
   TC_FLAG_EXACT_SUM = 32u /* indextts without verification outputs: the row's decisions
                              were not settled by the interval on the log-sum and took the
                              exact sequential sum (informational; the id is the same) */
@@ -119,6 +120,9 @@ typedef struct tc_sample_params {
                                update_penalty_mask fused into the step; ids >= V are
                                ignored).  May equal d_pen_mask only when rows == 1:
                                the row reads the mask before it marks it.  NULL = off */
+  int32_t typical;          /* indextts: GenerateConfig.typical_sampling (generation.rs:649-651,
+                               apply_typical :196-248); 0 = off.  ABI version 3 */
+  double typical_mass;      /* indextts: GenerateConfig.typical_mass, in (0, 1) when typical */
 } tc_sample_params;
 
 /* Optional verification outputs (device pointers; pass NULL to skip).  Ids are

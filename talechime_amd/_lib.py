@@ -48,6 +48,8 @@ class SampleParams(C.Structure):
         ("d_add_mask", C.c_void_p),
         ("d_pen_mask", C.c_void_p),
         ("d_mark_mask", C.c_void_p),
+        ("typical", C.c_int32),
+        ("typical_mass", C.c_double),
     ]
 
 

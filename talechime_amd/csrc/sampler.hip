@@ -90,6 +90,7 @@ struct RowArgs {
   int fast;          // indextts, qwen: the streaming fast path applies (1 <= K <= 64 < V, sampling)
   float* mark;       // optional [V] penalty mask: set to 1.0 at each row's sampled id
   float* keep_scores;  // indextts beam step: the final score of each kept id, beside keep_ids
+  double typical_mass; // indextts: the typical warper's mass (k_idx_typical); 0 = off
 };
 
 // Writes a row's result.  A row sampled cleanly also marks its token in the
@@ -1032,9 +1033,233 @@ struct IdxGenLds {
   uint32_t out[4];
 };
 
+// The typical warper (generation.rs:196-248, TypicalLogitsWarper) on the
+// penalised log-probs x, in place: ids whose |(-nz) - ent| exceeds that of
+// the first id (in ascending order of it, ties by id) at which the running
+// softmax mass reaches `mass` are set to -inf.  nz = log_softmax(x) and the
+// expf in ent's terms are the reference's bits (exact_log_softmax,
+// expf_glibc); each term -(double)nz * (double)expf(nz) is exact in f64.
+//
+// The reference's f64 sums (ent in index order; the softmax denominator and
+// the running mass in the sorted order) are not reproduced; the cut is
+// certified instead.  ent is a block sum within E = (2V + 64) 2^-53 ent of the
+// reference's sequential one (non-negative terms), so each |(-nz) - ent|
+// is known within E plus an ulp.  The cut key theta comes from a radix
+// select over the bit patterns of |(-nz) - ent| (non-negative doubles order
+// as integers), weighted by exp(x - max): at each level the key range is cut
+// into 1024 bins, the bin where the weight below reaches mass * sum is kept.
+// The row is certified when (a) no id outside theta's group lies within the
+// uncertainty of theta and theta's group holds one nz value, and (b) the
+// weight strictly below theta is under mass * sum and the weight through
+// theta's group above it, each by (4V + 64) 2^-53 + 2^-46 of the sum (the
+// reference's f64 exp and sequential sums against these).  Otherwise the
+// cut is taken as computed and TC_FLAG_NEAR_TIE is returned.
+//
+// Rows with a NaN or +inf score keep every id: the reference's softmax is
+// NaN or all zero there, so its running mass never reaches `mass` and the
+// cut falls on the last id.  Returns the flags to add.
+template <int ITEMS>
+__device__ __forceinline__ uint32_t idx_typical(const RowArgs& a, float (&x)[ITEMS], uint32_t vm, int e0,
+                                             IdxGenLds& G) {
+  BlockScratch& s = G.s;
+  double* bw = G.sv.w;      // [1024] bin weights (the survivor stage is free until compaction)
+  uint32_t* bc = G.sv.idx;  // [1024] bin counts
+  uint64_t* m64 = G.sv.key; // [0] range low, [1] range high, [2] chosen bin, [3] nz bits min, [4] max
+  double* md = reinterpret_cast<double*>(G.sv.key + 8);  // [0] weight below the chosen bin
+  const int t = threadIdx.x, bd = (int)blockDim.x, V = a.V;
+  uint32_t bad = 0, fin = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((vm >> i) & 1u) {
+      bad |= (__builtin_isnan(x[i]) || x[i] == __builtin_inff()) ? 1u : 0u;
+      fin |= x[i] != -__builtin_inff() ? 1u : 0u;
+    }
+  bad = block_or_u(bad, s);
+  fin = block_or_u(fin, s);
+  if (bad || !fin) return 0u;
+  // nz and the entropy's terms
+  float nz[ITEMS];
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) nz[i] = x[i];
+  exact_log_softmax<ITEMS>(nz, vm, e0, G.sq, G.sc, s, reinterpret_cast<float*>(&G.sv), V);
+  double part = 0.0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && nz[i] != -__builtin_inff()) part += -(double)nz[i] * (double)expf_glibc(nz[i]);
+  double ent;
+  (void)block_excl_scan_d(part, G.sc, &ent);
+  const double e_ent = (double)(2 * V + 64) * 0x1p-53 * ent + 0x1p-1000;
+  auto key_of = [&](float z) { return (uint64_t)__double_as_longlong(fabs(-(double)z - ent)); };
+  // weights exp(x - max) in f64 (the reference's softmax_f64 numerators)
+  double w[ITEMS];
+  double mx = -__builtin_inf();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((vm >> i) & 1u) mx = rmaxd(mx, (double)x[i]);
+  mx = block_max_d(mx, s);
+  double wpart = 0.0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    w[i] = ((vm >> i) & 1u) ? tc_exp_d((double)x[i] - mx) : 0.0;
+    wpart += w[i];
+  }
+  double wsum;
+  (void)block_excl_scan_d(wpart, G.sc, &wsum);
+  const double target = a.typical_mass * wsum;
+  // the range of the keys
+  uint64_t klo = ~0ull, khi = 0;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if ((vm >> i) & 1u) {
+      const uint64_t k = key_of(nz[i]);
+      klo = k < klo ? k : klo;
+      khi = k > khi ? k : khi;
+    }
+  if (t == 0) {
+    m64[0] = ~0ull;
+    m64[1] = 0;
+    md[0] = 0.0;
+  }
+  __syncthreads();
+  if (klo != ~0ull) {
+    atomicMin(reinterpret_cast<unsigned long long*>(&m64[0]), (unsigned long long)klo);
+    atomicMax(reinterpret_cast<unsigned long long*>(&m64[1]), (unsigned long long)khi);
+  }
+  __syncthreads();
+  const uint64_t kmax_all = m64[1];
+  uint64_t theta = kmax_all;  // no crossing: the cut falls on the last id
+  for (int level = 0; level < 8; ++level) {
+    const uint64_t lo = m64[0], hi = m64[1];
+    const double below = md[0];
+    if (lo == hi) {
+      theta = lo;
+      break;
+    }
+    const uint64_t span = hi - lo;
+    const int sh = (64 - __builtin_clzll(span)) > 10 ? (64 - __builtin_clzll(span)) - 10 : 0;
+    for (int b = t; b < 1024; b += bd) {
+      bw[b] = 0.0;
+      bc[b] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i) {
+      if (!((vm >> i) & 1u)) continue;
+      const uint64_t k = key_of(nz[i]);
+      if (k < lo || k > hi) continue;
+      const uint32_t b = (uint32_t)((k - lo) >> sh);
+      atomicAdd(&bw[b], w[i]);
+      atomicAdd(&bc[b], 1u);
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+      // lane l takes bins 16 l .. 16 l + 15
+      const int l = lane_id();
+      double lw = 0.0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) lw += bw[16 * l + j];
+      const double inc = wave_incl_scan_d(lw);
+      double run = below + (inc - lw);
+      int found = -1;
+      double before = 0.0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const double nr = run + bw[16 * l + j];
+        if (found < 0 && bc[16 * l + j] > 0u && nr >= target) {
+          found = 16 * l + j;
+          before = run;
+        }
+        run = nr;
+      }
+      const uint64_t hit = __ballot(found >= 0);
+      if (l == 0) m64[2] = hit ? (uint64_t)0 : ~0ull;
+      if (hit && l == __builtin_ctzll(hit)) {
+        m64[2] = (uint64_t)found;
+        md[0] = before;
+      }
+    }
+    __syncthreads();
+    const uint64_t bsel = m64[2];
+    if (bsel == ~0ull) {  // the whole row stays below the mass
+      theta = kmax_all;
+      break;
+    }
+    const uint64_t nlo = lo + (bsel << sh);
+    const uint64_t nhi = (sh + 10 >= 64 || ((bsel + 1) << sh) - 1 > hi - lo) ? hi : lo + ((bsel + 1) << sh) - 1;
+    __syncthreads();
+    if (t == 0) {
+      m64[0] = ~0ull;
+      m64[1] = 0;
+    }
+    __syncthreads();
+    klo = ~0ull;
+    khi = 0;
+#pragma unroll
+    for (int i = 0; i < ITEMS; ++i)
+      if ((vm >> i) & 1u) {
+        const uint64_t k = key_of(nz[i]);
+        if (k >= nlo && k <= nhi) {
+          klo = k < klo ? k : klo;
+          khi = k > khi ? k : khi;
+        }
+      }
+    if (klo != ~0ull) {
+      atomicMin(reinterpret_cast<unsigned long long*>(&m64[0]), (unsigned long long)klo);
+      atomicMax(reinterpret_cast<unsigned long long*>(&m64[1]), (unsigned long long)khi);
+    }
+    __syncthreads();
+  }
+  // certification: the weights below and through theta's group, the ids near
+  // theta, the nz values inside the group
+  const double th = __longlong_as_double((long long)theta);
+  const double band = 2.0 * (e_ent + th * 0x1p-52) + 0x1p-1000;
+  double wlt = 0.0, weq = 0.0;
+  uint32_t amb = 0, zlo = ~0u, zhi = 0u;
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    if (!((vm >> i) & 1u)) continue;
+    const uint64_t k = key_of(nz[i]);
+    const double sh_i = __longlong_as_double((long long)k);
+    if (k < theta) wlt += w[i];
+    if (k == theta) {
+      weq += w[i];
+      const uint32_t zb = __float_as_uint(nz[i]);
+      zlo = zb < zlo ? zb : zlo;
+      zhi = zb > zhi ? zb : zhi;
+    } else if (fabs(sh_i - th) <= band) {
+      amb = 1u;
+    }
+  }
+  if (t == 0) {
+    m64[3] = ~0ull;
+    m64[4] = 0;
+  }
+  double wlt_all, weq_all;
+  (void)block_excl_scan_d(wlt, G.sc, &wlt_all);
+  (void)block_excl_scan_d(weq, G.sc, &weq_all);
+  if (zlo != ~0u) {
+    atomicMin(reinterpret_cast<unsigned long long*>(&m64[3]), (unsigned long long)zlo);
+    atomicMax(reinterpret_cast<unsigned long long*>(&m64[4]), (unsigned long long)zhi);
+  }
+  amb = block_or_u(amb, s);
+  const double marg = ((double)(4 * V + 64) * 0x1p-53 + 0x1p-46) * wsum;
+  bool certain = !amb && m64[3] == m64[4];
+  if (theta == kmax_all && wlt_all + weq_all < target) {
+    certain = certain && wlt_all + weq_all <= target - marg;  // no crossing
+  } else {
+    certain = certain && wlt_all <= target - marg && wlt_all + weq_all >= target + marg;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && key_of(nz[i]) > theta) x[i] = -__builtin_inff();
+  return certain ? 0u : (uint32_t)TC_FLAG_NEAR_TIE;
+}
+
 // General path: any K, non-finite scores, more candidates than the fast path
-// stages.  Survivors of the top-k cut are staged in LDS (at most kSurvCap).
-template <typename InT, int ITEMS>
+// stages, the typical warper (TYPICAL: k_idx_typical).  Survivors of the
+// top-k cut are staged in LDS (at most kSurvCap).
+template <typename InT, int ITEMS, bool TYPICAL = false>
 __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
   uint8_t* s_seen = G.seen;
   SurvLds& sv = G.sv;
@@ -1053,15 +1278,20 @@ __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
   if (a.do_pen) build_seen(a, row, s_seen, s);
   const float log_sum = exact_log_softmax<ITEMS>(x, vm, e0, sq, sc, s, reinterpret_cast<float*>(&sv), V);
   put_norm(a, row, log_sum);
-  // repetition penalty on the log-probs (generation.rs:122-134), temperature (137-142)
+  // repetition penalty on the log-probs (generation.rs:122-134), the typical
+  // warper (:649-651), temperature (137-142)
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    if (!((vm >> i) & 1u)) continue;
-    float v = x[i];
-    if (a.do_pen && s_seen[e0 + i]) v = v < 0.0f ? v * a.pen_f : v / a.pen_f;
-    if (a.do_temp) v = v / a.t_f;
-    x[i] = v;
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && a.do_pen && s_seen[e0 + i]) x[i] = x[i] < 0.0f ? x[i] * a.pen_f : x[i] / a.pen_f;
+  uint32_t row_flags = 0;
+  if constexpr (TYPICAL) {
+    __syncthreads();
+    row_flags = idx_typical<ITEMS>(a, x, vm, e0, G);
+    __syncthreads();
   }
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i)
+    if (((vm >> i) & 1u) && a.do_temp) x[i] = x[i] / a.t_f;
   // general path: radix select over the whole row, survivors staged in LDS
   float kth = -__builtin_inff();
   bool cut = false;
@@ -1082,7 +1312,7 @@ __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
   const uint32_t n = compact<ITEMS>(x, surv, e0, sv, s);
   if (n > (uint32_t)kSurvCap) {
     write_topk(a, row, sv, n);
-    finish_row(a, row, 0u, TC_EUNSUPPORTED, 0u);
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
     if (t == 0 && a.keep_count) a.keep_count[row] = 0;
     return;
   }
@@ -1156,7 +1386,7 @@ __device__ __forceinline__ void idx_general(const RowArgs& a, IdxGenLds& G) {
       }
       tok = sv.idx[pick != 0xffffffffu ? pick : last];
     }
-    put_result(a, row, tok, st, 0u);
+    put_result(a, row, tok, st, row_flags);
     s_out[0] = nl;
   }
   if (a.keep_count) {
@@ -2162,6 +2392,14 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       a.keep_count[row] = tk;
     }
   }
+}
+
+// indextts with the typical warper (generation.rs:649-651, off by default):
+// the general path with idx_typical between the penalty and the temperature.
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_idx_typical(RowArgs a) {
+  __shared__ IdxGenLds G;
+  idx_general<InT, ITEMS, true>(a, G);
 }
 
 // ================================================================ cosyvoice3
@@ -3588,6 +3826,7 @@ bool pick_shape(int V, int dtype, int* items, int* threads) {
 
 TC_DEFINE_LAUNCH(k_qwen)
 TC_DEFINE_LAUNCH(k_indextts)
+TC_DEFINE_LAUNCH(k_idx_typical)
 TC_DEFINE_LAUNCH(k_cosy)
 TC_DEFINE_LAUNCH(k_moss)
 TC_DEFINE_LAUNCH(k_nano)
@@ -3811,7 +4050,11 @@ static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, 
       }
       a.do_topp = p->top_p < 1.0;
       a.top_p_d = p->top_p;
-      a.fast = a.K >= 1 && a.K <= 64 && a.K < V && a.min_keep <= a.K;
+      if (p->typical) {  // GenerateConfig.typical_mass, checked as typical_sampling's mass
+        if (!(p->typical_mass > 0.0 && p->typical_mass < 1.0)) return fail(TC_EINVAL, "typical_mass must be in (0, 1)");
+        a.typical_mass = p->typical_mass;
+      }
+      a.fast = a.K >= 1 && a.K <= 64 && a.K < V && a.min_keep <= a.K && !p->typical;
       break;
     }
     case TC_MOSS: {
@@ -3860,7 +4103,10 @@ static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, 
   switch (p->variant) {
     case TC_QWEN: e = launch_k_qwen(dtype, items, threads, (int)rows, st, a); break;
     case TC_COSY_RAS: e = launch_k_cosy(dtype, items, threads, (int)rows, st, a); break;
-    case TC_INDEXTTS: e = launch_k_indextts(dtype, items, threads, (int)rows, st, a); break;
+    case TC_INDEXTTS:
+      e = a.typical_mass > 0.0 ? launch_k_idx_typical(dtype, items, threads, (int)rows, st, a)
+                               : launch_k_indextts(dtype, items, threads, (int)rows, st, a);
+      break;
     case TC_MOSS: e = launch_k_moss(dtype, items, threads, (int)rows, st, a); break;
     default: e = launch_k_nano(dtype, items, threads, (int)rows, st, a); break;
   }

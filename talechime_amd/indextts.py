@@ -2,8 +2,9 @@
 
     GenerateConfig                          generation.rs:43-72 (same defaults)
     sample_rows(logits, input_ids, cfg, uniforms)
-        the row processors (log_softmax, repetition penalty, temperature,
-        top-k, top-p; generation.rs:643-662) and one draw of
+        the row processors (log_softmax, repetition penalty, the typical
+        warper when cfg.typical_sampling, temperature, top-k, top-p;
+        generation.rs:643-662) and one draw of
         sample_without_replacement (280-303) per row
     beam_step(logits, input_ids, beam_scores, cfg, uniforms)
         one step of the beam-sample loop (619-701): the joint scores and the
@@ -14,8 +15,7 @@
 The reference draws its f64 uniforms from rand's StdRng, which is not
 reproduced here: callers pass the uniforms (``rng.unit_f64`` gives the same
 mapping of 64-bit outputs to [0, 1)).  ``input_ids`` are the per-row id
-lists the penalty reads.  The typical warper (cfg.typical_sampling) has no
-device path and raises.
+lists the penalty reads.
 """
 from __future__ import annotations
 
@@ -47,10 +47,9 @@ class GenerateConfig:
 
 
 def _params(cfg: GenerateConfig):
-    if cfg.typical_sampling:
-        raise NotImplementedError("the typical warper (generation.rs:196-248) has no device path")
     return make_params(_lib.INDEXTTS, temperature=cfg.temperature, top_k=cfg.top_k, top_p=cfg.top_p,
-                       penalty=cfg.repetition_penalty, min_keep=2)
+                       penalty=cfg.repetition_penalty, min_keep=2, typical=cfg.typical_sampling,
+                       typical_mass=cfg.typical_mass)
 
 
 def _uniforms(u, n: int, dev) -> torch.Tensor:

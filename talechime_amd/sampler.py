@@ -23,16 +23,19 @@ def make_params(variant: int, *, temperature: float = 1.0, top_p: float = 1.0, p
                 top_k: int = 0, min_keep: int = 2, ras_win: int = 10, ras_tau: float = 0.1,
                 eos_id: int = -1, exclude_id: int = -1, hist_mode: int = HIST_PER_ROW,
                 add_mask: torch.Tensor | None = None, pen_mask: torch.Tensor | None = None,
-                mark_mask: torch.Tensor | None = None) -> SampleParams:
+                mark_mask: torch.Tensor | None = None, typical: bool = False,
+                typical_mass: float = 0.9) -> SampleParams:
     """Parameters of one sampler step.  `mark_mask` ([V] f32 on the device)
     receives 1.0 at each cleanly sampled row's id, the penalty-mask update of
     synthesis.rs:568-579 fused into the step; it may be `pen_mask` itself for a
-    one-row step."""
+    one-row step.  `typical` / `typical_mass`: indextts's typical warper
+    (GenerateConfig.typical_sampling / typical_mass)."""
     p = SampleParams()
     p.variant, p.hist_mode = variant, hist_mode
     p.temperature, p.top_p, p.repetition_penalty = float(temperature), float(top_p), float(penalty)
     p.top_k, p.min_keep, p.ras_win, p.ras_tau = int(top_k), int(min_keep), int(ras_win), float(ras_tau)
     p.eos_id, p.exclude_id = int(eos_id), int(exclude_id)
+    p.typical, p.typical_mass = int(bool(typical)), float(typical_mass)
     if add_mask is not None:
         _need_cuda(add_mask, torch.float32, "add_mask")
         p.d_add_mask = add_mask.data_ptr()

@@ -29,7 +29,7 @@ def test_library_exports_every_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     lib.tc_abi_version.restype = ctypes.c_int
-    assert lib.tc_abi_version() == 2
+    assert lib.tc_abi_version() == 3
 
 
 def _c_layout(struct: str, fields):

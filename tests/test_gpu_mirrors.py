@@ -114,9 +114,12 @@ def test_indextts_rows_and_beam_steps(dev):
     os_ = O.idx_beam_search_step(O.make_params(O.INDEXTTS, **kw), bb.logits, bb.hist_off, bb.hist_ids,
                                  bb.beam_scores, 3, 6)
     assert np.array_equal(cs.flat.cpu().numpy().view(np.uint32), os_["flat"])
-    with pytest.raises(NotImplementedError):
-        it.sample_rows(torch.from_numpy(b.logits).to(dev), hist, it.GenerateConfig(typical_sampling=True),
-                       b.uniforms)
+    # the typical warper (typical_sampling) runs between the penalty and the temperature
+    tcfg = it.GenerateConfig(typical_sampling=True, typical_mass=0.7)
+    ids = it.sample_rows(torch.from_numpy(b.logits).to(dev), hist, tcfg, b.uniforms).cpu().numpy().view(np.uint32)
+    o = O.sample(O.make_params(O.INDEXTTS, typical=True, typical_mass=0.7, **kw), b.logits_f32, b.hist_off,
+                 b.hist_ids, b.uniforms)
+    assert ids.tolist() == o["ids"].tolist()
 
 
 def test_moss_sample_and_nano_sampler(dev):
