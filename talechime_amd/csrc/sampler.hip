@@ -1459,13 +1459,6 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
     for (int w = t; w < nwords; w += blockDim.x) F.bits[w] = 0u;
     if (t < 64) F.bins[t] = 0u;
     lds_barrier();
-#pragma unroll
-    for (int j = 0; j < kHpt; ++j)
-      if (hid[j] < (uint32_t)V) atomicOr(&F.bits[hid[j] >> 5], 1u << (hid[j] & 31u));
-    for (uint32_t k = h0 + (uint32_t)t + (uint32_t)kHpt * blockDim.x; k < h1; k += blockDim.x) {
-      const uint32_t id = a.hist_ids[k];
-      if (id < (uint32_t)V) atomicOr(&F.bits[id >> 5], 1u << (id & 31u));
-    }
     const uint32_t vm = valid_mask<ITEMS>(V, shift);
     const int e0 = t * ITEMS - shift;
     // row max; the sum of the row is finite iff every logit is (or overflows:
@@ -1491,14 +1484,15 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       fin = dpp_wave_sum(in ? F.wfin[lane_id()] : 0.0f);
     }
     if (__builtin_isfinite(fin) && __builtin_isfinite(mx)) {
-      // ids in the history, bit i = element e0 + i
-      uint64_t seen = 0;
-      if (a.do_pen) {
-        const int w0 = e0 >= 0 ? (e0 >> 5) : 0;
-        const uint32_t lo = w0 < nwords ? F.bits[w0] : 0u;
-        const uint32_t hi = w0 + 1 < nwords ? F.bits[w0 + 1] : 0u;
-        seen = ((((uint64_t)hi << 32) | lo) >> (e0 >= 0 ? (e0 & 31) : 0));
-        if (e0 < 0) seen <<= (uint32_t)(-e0);
+      // the history bitmap, its ids' loads (two dependent rounds: offsets,
+      // then ids) overlapping the max and the terms below; read after the
+      // terms' barrier
+#pragma unroll
+      for (int j = 0; j < kHpt; ++j)
+        if (hid[j] < (uint32_t)V) atomicOr(&F.bits[hid[j] >> 5], 1u << (hid[j] & 31u));
+      for (uint32_t k = h0 + (uint32_t)t + (uint32_t)kHpt * blockDim.x; k < h1; k += blockDim.x) {
+        const uint32_t id = a.hist_ids[k];
+        if (id < (uint32_t)V) atomicOr(&F.bits[id >> 5], 1u << (id & 31u));
       }
       // log_softmax (generation.rs:95-105): d = x - max; S = sequential f32 sum of exp(d)
       float d[ITEMS], ap[ITEMS];
@@ -1518,10 +1512,8 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       for (int i = 0; i < ITEMS; ++i) {
         const bool v = (vm >> i) & 1u;
         d[i] = x[i] - mx;
-        if (v && !((seen >> i) & 1ull)) mns = mns > d[i] ? mns : d[i];
         if (cert_mode) tsum += v ? __builtin_amdgcn_exp2f(d[i] * 1.44269504088896341f) : 0.0f;
       }
-      if (mns > -16.0f) atomicAdd(&F.bins[(uint32_t)(-mns * 4.0f)], 1u);
       SeqSum<ITEMS> sq;
       // the exact sum's approximate terms and their prediction (SeqSum)
       auto exact_terms = [&]() {
@@ -1540,6 +1532,21 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
       } else {
         exact_terms();
       }
+      lds_barrier();
+      // ids in the history, bit i = element e0 + i, and the histogram of the
+      // per-thread maxima of d over the others
+      uint64_t seen = 0;
+      if (a.do_pen) {
+        const int w0 = e0 >= 0 ? (e0 >> 5) : 0;
+        const uint32_t lo = w0 < nwords ? F.bits[w0] : 0u;
+        const uint32_t hi = w0 + 1 < nwords ? F.bits[w0 + 1] : 0u;
+        seen = ((((uint64_t)hi << 32) | lo) >> (e0 >= 0 ? (e0 & 31) : 0));
+        if (e0 < 0) seen <<= (uint32_t)(-e0);
+      }
+#pragma unroll
+      for (int i = 0; i < ITEMS; ++i)
+        if (((vm >> i) & 1u) && !((seen >> i) & 1ull)) mns = mns > d[i] ? mns : d[i];
+      if (mns > -16.0f) atomicAdd(&F.bins[(uint32_t)(-mns * 4.0f)], 1u);
       lds_barrier();
       // Candidates, staged while the exact sum is finished.  The histogram of
       // per-thread maxima of d over ids not in the history puts the K-th largest
