@@ -1695,8 +1695,8 @@ __global__ void __launch_bounds__(max_threads(ITEMS)) k_indextts(RowArgs a) {
 //    threshold; at most kLargeCand), staged in vocabulary order a tile at a
 //    time.
 //  * Rows these passes do not decide (non-finite logits, a negative penalty,
-//    a K-th key more than 256 keys below the largest) take large_general,
-//    which streams the row from memory again and selects by logit.
+//    a K-th key more than 256 keys below the largest) take large_candidates,
+//    which streams the row from memory again and selects on the final logits.
 //  * A bitonic sort gives the reference's rank order (value descending, id
 //    ascending); top-k keeps every value >= the k-th (ties kept).
 //  * top-p: exact terms, the reference's sequential f32 sum in rank order and
@@ -1832,134 +1832,191 @@ __device__ __forceinline__ float qlogit(const RowArgs& a, float x, bool sn, int 
   return v;
 }
 
-// Candidates of the rows whose selection the register-tiled passes of
-// k_qwen_large do not decide: a non-finite logit, a negative penalty (the
-// penalised logit then falls as the bf16 value rises), a K-th largest key
-// more than 256 keys below the largest, or a K-th logit that overflowed to
-// -inf.  The row is streamed from memory again, in up to four passes:
-//  1. (non-finite rows) NaN and +inf after the caller chain, and the largest
-//     key outside the history over the ids whose logit is not NaN;
-//  2.-3. (K-th key not known) a radix select of the K-th largest key outside
-//     the history over its 16-bit distance below the largest, high byte
-//     first (runs of equal bins added at once), then the low byte;
-//  4. every id whose logit is not NaN and reaches the K-th key's logit (a
-//     superset of the reference's top-k survivors: the K-th logit over all
-//     ids is at least the K-th over those outside the history), staged in
-//     vocabulary order in S.cand and S.candv.
-// kmax and bK are the largest key outside the history and the K-th key's
-// distance below it when the caller knows them (bK 0xffffffff otherwise).
-// Returns the candidate count (the first kLargeCand staged), 0xffffffff when
-// a logit is +inf, and kLargeCand + 1 when fewer than K ids lie outside the
-// history.  NaN logits are left out and the row flagged TC_FLAG_NAN_ROW:
-// the reference's order for them at top-k is unspecified.
-__device__ __forceinline__ uint32_t large_general(const RowArgs& a, QLargeLds& S, const uint4* base, int nchunks,
-                                                 int shift, int eos, uint32_t kmax, uint32_t bK, bool nonfinite,
-                                                 uint32_t* row_flags) {
+// The logit of element e with every option of the caller chain
+// (synthesis.rs:1238-1276) and the temperature (sampling.rs:175-184): the
+// penalty on ids in the history bitmap (hist_bit) or, in TC_HIST_MASK mode,
+// on ids whose [V] mask entry is > 0; the additive mask; the EOS id forced
+// to -inf; the multiply by f32(1/T).
+__device__ __forceinline__ float qlogit_all(const RowArgs& a, float x, bool hist_bit, int e, int eos) {
+  float v = x;
+  if (a.do_pen) {
+    const bool pen = a.hist_mode == TC_HIST_MASK ? a.pen_mask[e] > 0.0f : hist_bit;
+    if (pen) v = v * (v > 0.0f ? a.inv_pen : a.pen_f);
+  }
+  if (a.add_mask) v = v + a.add_mask[e];
+  if (e == eos) v = -__builtin_inff();
+  if (a.do_temp) v = v * a.tmul + 0.0f;
+  return v;
+}
+
+// Element h of a 16-byte chunk of a bf16 or f32 row, as f32.
+template <typename InT>
+__device__ __forceinline__ float chunk_val(const uint4& v, int h) {
+  if constexpr (sizeof(InT) == 2) {
+    const uint32_t w = u4_word(v, h >> 1);
+    return __uint_as_float((h & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return __uint_as_float(u4_word(v, h));
+  }
+}
+
+// A row of a large-vocabulary launch as 16-byte chunks: chunk q holds
+// elements q * kEpc - shift .. q * kEpc - shift + kEpc - 1.
+template <typename InT>
+struct LargeRow {
+  static constexpr int kEpc = 16 / (int)sizeof(InT);
+  const uint4* base;
+  int shift, nchunks;
+  __device__ __forceinline__ LargeRow(const RowArgs& a, int row) {
+    const InT* rp = reinterpret_cast<const InT*>(a.logits) + (size_t)row * (size_t)a.ld;
+    shift = (int)((reinterpret_cast<uintptr_t>(rp) / sizeof(InT)) & (uintptr_t)(kEpc - 1));
+    base = reinterpret_cast<const uint4*>(rp - shift);
+    nchunks = (a.V + shift + kEpc - 1) / kEpc;
+  }
+};
+
+// The 16-bit key of a logit (ckey's high half): monotone non-decreasing in
+// the value, both zeros at 0x8000, -inf at 0x007f.
+__device__ __forceinline__ uint32_t key16(float v) { return ckey(v) >> 16; }
+
+// Candidates of a large-vocabulary qwen row selected on its final logits:
+// every option of the caller chain (penalty from the history or a mask, the
+// additive mask, EOS, temperature, a penalty of either sign), bf16 or f32
+// rows, non-finite values.  The row is streamed from memory, four passes:
+//  1. NaN and +inf logits, and the largest key16 over the logits not NaN;
+//  2.-3. a radix select of the K-th largest key16 over its 16-bit distance
+//     below the largest, high byte first (runs of equal bins added at once),
+//     then the low byte inside the chosen bin;
+//  4. every id whose logit is not NaN and reaches the smallest value of the
+//     K-th key's bin (at most the K-th largest logit: a superset of the
+//     reference's top-k survivors), staged in vocabulary order in S.cand and
+//     S.candv.
+// With fewer than K logits not NaN every one of them is a candidate.
+// Returns the candidate count (the first kLargeCand staged), or 0xffffffff
+// when a logit is +inf.  NaN logits are left out and the row flagged
+// TC_FLAG_NAN_ROW: the reference's order for them at top-k is unspecified.
+// The history bitmap (S.bits) must be built when the penalty reads it.
+template <typename InT>
+__device__ __forceinline__ uint32_t large_candidates(const RowArgs& a, QLargeLds& S, int row, int eos,
+                                                     uint32_t* row_flags) {
+  constexpr int E = LargeRow<InT>::kEpc;
+  const LargeRow<InT> R(a, row);
   const int t = threadIdx.x, V = a.V, nwords = (V + 31) >> 5;
   const int tile = kLargeU * (int)blockDim.x;
   const uint32_t K = (uint32_t)a.K;
+  const bool use_bits = a.do_pen && a.hist_mode != TC_HIST_MASK;
   // every chunk once, thread t taking chunks tb + kLargeU * t + u of each tile
   // (vocabulary order within the tile); the tile count is the same for all
   auto walk = [&](auto&& body) __attribute__((always_inline)) {
-    for (int tb = 0; tb < nchunks; tb += tile) {
+    for (int tb = 0; tb < R.nchunks; tb += tile) {
       uint4 raw[kLargeU];
 #pragma unroll
-      for (int u = 0; u < kLargeU; ++u) raw[u] = base[min(tb + kLargeU * t + u, nchunks - 1)];
+      for (int u = 0; u < kLargeU; ++u) raw[u] = R.base[min(tb + kLargeU * t + u, R.nchunks - 1)];
       body(raw, tb);
     }
   };
-  if (nonfinite) {
-    uint32_t nan = 0, pinf = 0, km = 0;
+  // the logits of chunk q (bit h of the result: element h lies in the row)
+  auto logits = [&](const uint4& v, int q, float (&lv)[E]) __attribute__((always_inline)) -> uint32_t {
+    const int c0 = q * E - R.shift;
+    const uint32_t hb = use_bits ? bits_at_fn(S.bits, nwords, c0) : 0u;
+    uint32_t in = 0;
+#pragma unroll
+    for (int h = 0; h < E; ++h) {
+      const int e = c0 + h;
+      const bool ok = e >= 0 && e < V;
+      in |= (ok ? 1u : 0u) << h;
+      lv[h] = ok ? qlogit_all(a, chunk_val<InT>(v, h), ((hb >> h) & 1u) != 0u, e, eos) : 0.0f;
+    }
+    return in;
+  };
+  // pass 1
+  uint32_t nan = 0, pinf = 0, km = 0;
+  walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kLargeU; ++u) {
+      const int q = tb + kLargeU * t + u;
+      if (q >= R.nchunks) break;
+      float lv[E];
+      const uint32_t in = logits(raw[u], q, lv);
+#pragma unroll
+      for (int h = 0; h < E; ++h) {
+        if (!((in >> h) & 1u)) continue;
+        if (__builtin_isnan(lv[h])) {
+          nan = 1u;
+          continue;
+        }
+        pinf |= lv[h] == __builtin_inff() ? 1u : 0u;
+        km = max(km, key16(lv[h]));
+      }
+    }
+  });
+  const bool any_nan = block_or_u(nan, S.s) != 0u;
+  pinf = block_or_u(pinf, S.s);
+  const uint32_t kmax = block_max_u(km, S.s);
+  if (any_nan) *row_flags |= TC_FLAG_NAN_ROW;
+  if (pinf) return 0xffffffffu;
+  // passes 2-3
+  uint32_t bK = 0xffffffffu, hi = 0;
+  for (int lvl = 0; lvl < 2; ++lvl) {
+    if (t < 256) S.hist[t] = 0u;
+    __syncthreads();
     walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+      uint32_t run_bin = 0xffffffffu, run_n = 0;
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
-        if (q >= nchunks) break;
-        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+        if (q >= R.nchunks) break;
+        float lv[E];
+        const uint32_t in = logits(raw[u], q, lv);
 #pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const int e = q * 8 - shift + h;
-          if (e < 0 || e >= V) continue;
-          const bool sn = (c.sn >> h) & 1u;
-          const float lv = qlogit(a, c.x[h], sn, e, eos);
-          if (__builtin_isnan(lv)) {
-            nan = 1u;
-            continue;
+        for (int h = 0; h < E; ++h) {
+          if (!((in >> h) & 1u) || __builtin_isnan(lv[h])) continue;
+          const uint32_t dist = kmax - key16(lv[h]);
+          if (lvl == 1 && (dist >> 8) != hi) continue;
+          const uint32_t bin = lvl == 0 ? (dist >> 8) : (dist & 0xffu);
+          if (bin != run_bin) {
+            if (run_n) atomicAdd(&S.hist[run_bin], run_n);
+            run_bin = bin;
+            run_n = 0;
           }
-          pinf |= lv == __builtin_inff() ? 1u : 0u;
-          if (!sn) km = max(km, ckey(c.x[h]) >> 16);
+          ++run_n;
         }
       }
+      if (run_n) atomicAdd(&S.hist[run_bin], run_n);
     });
-    const bool any_nan = block_or_u(nan, S.s) != 0u;
-    pinf = block_or_u(pinf, S.s);
-    kmax = block_max_u(km, S.s);
-    if (any_nan) *row_flags |= TC_FLAG_NAN_ROW;
-    if (pinf) return 0xffffffffu;
-    bK = 0xffffffffu;
-  }
-  if (bK == 0xffffffffu) {
-    uint32_t hi = 0;
-    for (int lvl = 0; lvl < 2; ++lvl) {
-      if (t < 256) S.hist[t] = 0u;
-      __syncthreads();
-      walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
-        uint32_t run_bin = 0xffffffffu, run_n = 0;
-#pragma unroll
-        for (int u = 0; u < kLargeU; ++u) {
-          const int q = tb + kLargeU * t + u;
-          if (q >= nchunks) break;
-          const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
-#pragma unroll
-          for (int h = 0; h < 8; ++h) {
-            const int e = q * 8 - shift + h;
-            // outside the history, inside the row, not NaN (such a logit is
-            // NaN exactly when its bf16 value is)
-            if (e < 0 || e >= V || ((c.sn >> h) & 1u) || __builtin_isnan(c.x[h])) continue;
-            const uint32_t dist = kmax - (ckey(c.x[h]) >> 16);
-            if (lvl == 1 && (dist >> 8) != hi) continue;
-            const uint32_t bin = lvl == 0 ? (dist >> 8) : (dist & 0xffu);
-            if (bin != run_bin) {
-              if (run_n) atomicAdd(&S.hist[run_bin], run_n);
-              run_bin = bin;
-              run_n = 0;
-            }
-            ++run_n;
-          }
-        }
-        if (run_n) atomicAdd(&S.hist[run_bin], run_n);
-      });
-      __syncthreads();
-      // the bin holding the K-th: the high level counts from the largest
-      // key, the low level what the higher bins left
-      const uint32_t need = lvl == 0 ? K : S.misc[1];
-      if (wave_id() == 0) {
-        const int l = lane_id();
-        const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
-        const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
-        uint32_t b = 0xffffffffu, before = 0;
-        if (ex + h0 >= need) { b = 4 * l; before = ex; }
-        else if (ex + h0 + h1 >= need) { b = 4 * l + 1; before = ex + h0; }
-        else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
-        else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
-        const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
-        if (l == 0) {
-          const int w = m ? __builtin_ctzll(m) : 0;
-          S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
-          S.misc[1] = m ? need - rl_u32(before, w) : 0u;
-        }
+    __syncthreads();
+    // the bin holding the K-th: the high level counts from the largest key,
+    // the low level what the higher bins left
+    const uint32_t need = lvl == 0 ? K : S.misc[1];
+    if (wave_id() == 0) {
+      const int l = lane_id();
+      const uint32_t h0 = S.hist[4 * l], h1 = S.hist[4 * l + 1], h2 = S.hist[4 * l + 2], h3 = S.hist[4 * l + 3];
+      const uint32_t inc = dpp_scan_u32(h0 + h1 + h2 + h3), ex = inc - (h0 + h1 + h2 + h3);
+      uint32_t b = 0xffffffffu, before = 0;
+      if (ex + h0 >= need) { b = 4 * l; before = ex; }
+      else if (ex + h0 + h1 >= need) { b = 4 * l + 1; before = ex + h0; }
+      else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
+      else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
+      const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
+      if (l == 0) {
+        const int w = m ? __builtin_ctzll(m) : 0;
+        S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
+        S.misc[1] = m ? need - rl_u32(before, w) : 0u;
       }
-      __syncthreads();
-      const uint32_t found = S.misc[0];
-      if (found == 0xffffffffu) return (uint32_t)kLargeCand + 1u;  // fewer than K ids outside the history
-      if (lvl == 0) hi = found;
-      else bK = (hi << 8) | found;
-      __syncthreads();
     }
+    __syncthreads();
+    const uint32_t found = S.misc[0];
+    __syncthreads();
+    if (found == 0xffffffffu) break;  // fewer than K logits not NaN: all are candidates
+    if (lvl == 0) hi = found;
+    else bK = (hi << 8) | found;
   }
-  const uint32_t keyK = kmax - bK;
-  const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
-  const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
+  float thr = -__builtin_inff();
+  if (bK != 0xffffffffu) {
+    const uint32_t keyK = kmax - bK;
+    thr = keyK <= 0x007fu ? -__builtin_inff() : untkey(keyK << 16);  // the smallest value with that key
+  }
+  // pass 4
   uint32_t n_c = 0;
   walk([&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
     uint32_t sel[kLargeU], cnt = 0;
@@ -1967,14 +2024,12 @@ __device__ __forceinline__ uint32_t large_general(const RowArgs& a, QLargeLds& S
     for (int u = 0; u < kLargeU; ++u) {
       sel[u] = 0u;
       const int q = tb + kLargeU * t + u;
-      if (q < nchunks) {
-        const LChunk c = decode_lchunk(raw[u], q, shift, V, S.bits, nwords, eos);
+      if (q < R.nchunks) {
+        float lv[E];
+        const uint32_t in = logits(raw[u], q, lv);
 #pragma unroll
-        for (int h = 0; h < 8; ++h) {
-          const int e = q * 8 - shift + h;
-          const float lv = qlogit(a, c.x[h], (c.sn >> h) & 1u, e, eos);
-          sel[u] |= (e >= 0 && e < V && !__builtin_isnan(lv) && lv >= thr) ? 1u << h : 0u;
-        }
+        for (int h = 0; h < E; ++h)
+          sel[u] |= (((in >> h) & 1u) && !__builtin_isnan(lv[h]) && lv[h] >= thr) ? 1u << h : 0u;
       }
       cnt += (uint32_t)__builtin_popcount(sel[u]);
     }
@@ -1982,17 +2037,15 @@ __device__ __forceinline__ uint32_t large_general(const RowArgs& a, QLargeLds& S
     uint32_t off = n_c + block_excl_scan(cnt, S.s, &tot);
 #pragma unroll
     for (int u = 0; u < kLargeU; ++u) {
-      const int c0 = (tb + kLargeU * t + u) * 8 - shift;
-      const uint32_t hb = sel[u] ? bits_at_fn(S.bits, nwords, c0) : 0u;
-      const uint32_t x = raw[u].x, y = raw[u].y, z = raw[u].z, w = raw[u].w;
-      for (uint32_t m = sel[u]; m; m &= m - 1u) {
-        const int h = __builtin_ctz(m);
-        const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
-        const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
-        const int e = c0 + h;
-        const float lv = qlogit(a, __uint_as_float(b), ((hb >> h) & 1u) != 0u || e == eos, e, eos);
+      if (!sel[u]) continue;
+      const int q = tb + kLargeU * t + u;
+      float lv[E];
+      (void)logits(raw[u], q, lv);
+#pragma unroll
+      for (int h = 0; h < E; ++h) {
+        if (!((sel[u] >> h) & 1u)) continue;
         if (off < (uint32_t)kLargeCand) {
-          const uint64_t kv = ((uint64_t)(~ckey(lv)) << 32) | (uint32_t)e;
+          const uint64_t kv = ((uint64_t)(~ckey(lv[h])) << 32) | (uint32_t)(q * E - R.shift + h);
           S.cand[off] = kv;
           S.candv[off] = kv;
         }
@@ -2002,6 +2055,130 @@ __device__ __forceinline__ uint32_t large_general(const RowArgs& a, QLargeLds& S
     n_c += tot;
   });
   return n_c;
+}
+
+
+// The finish of a large-vocabulary qwen row from its n_c candidates (S.cand
+// and S.candv in vocabulary order): the rank sort (value descending, id
+// ascending), top-k with ties kept (sampling.rs:224-249), top-p on exact terms
+// with the reference's sequential sums in rank order (:255-299), softmax and
+// the CDF in vocabulary order over the kept ids (:302-328).
+__device__ __forceinline__ void large_finish(const RowArgs& a, QLargeLds& S, int row, uint32_t n_c, uint32_t row_flags) {
+  const int t = threadIdx.x;
+  const uint32_t K = (uint32_t)a.K;
+  __syncthreads();
+  if (n_c > (uint32_t)kLargeCand) {
+    finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
+    no_verify(a, row);
+    return;
+  }
+  // rank order: more than 256 candidates sort as 2048 keys in registers
+  const int n_pad = n_c > 256u ? kLargeCand : next_pow2((int)n_c < 2 ? 2 : (int)n_c);
+  for (int j = (int)n_c + t; j < n_pad; j += blockDim.x) S.cand[j] = ~0ull;
+  __syncthreads();
+  if (n_pad == kLargeCand) block_sort2048(S.cand);
+  else block_bitonic_sort(S.cand, n_pad);
+  // top-k (sampling.rs:224-249): every value >= the K-th largest
+  const uint32_t kth_hi = (uint32_t)(S.cand[K - 1] >> 32);  // ~ckey of the K-th value
+  auto val_of = [](uint64_t kv) { return untkey(~(uint32_t)(kv >> 32)); };
+  uint32_t ns_part = 0;
+  for (int j = t; j < (int)n_c; j += blockDim.x) ns_part += (uint32_t)(S.cand[j] >> 32) <= kth_hi ? 1u : 0u;
+  const uint32_t ns = block_sum_u(ns_part, S.s);
+  const float vmax = val_of(S.cand[0]);
+  if (vmax == __builtin_inff()) {  // a finite value overflowing to +inf: as above
+    finish_row(a, row, 0u, TC_OK, row_flags);
+    no_verify(a, row);
+    return;
+  }
+  uint32_t flags = row_flags, cut = ns;
+  if (a.do_topp) {
+    // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential
+    // sum, running sum of e / S, cutoff at the first crossing (kept)
+    float e[kLargePer], pre[kLargePer];
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t r = kLargePer * t + q;
+      e[q] = r < ns ? expf_glibc(val_of(S.cand[r]) - vmax) : 0.0f;
+    }
+    float Sr = small_seq_prefix(e, pre, S);
+    float pq[kLargePer];
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) pq[q] = (kLargePer * t + q) < ns ? e[q] / Sr : 0.0f;
+    small_seq_prefix(pq, pre, S);
+    uint32_t first = 0xffffffffu;
+#pragma unroll
+    for (int q = kLargePer - 1; q >= 0; --q)
+      if ((kLargePer * t + q) < ns && pre[q] > a.top_p_f) first = kLargePer * t + q;
+    first = block_min_u(first, S.s);
+    if (first != 0xffffffffu) cut = first + 1;
+    if (cut < ns && (uint32_t)(S.cand[cut - 1] >> 32) == (uint32_t)(S.cand[cut] >> 32)) flags |= TC_FLAG_TIE_CUT;
+  }
+  const uint64_t last_kept = S.cand[cut - 1];
+  // softmax + multinomial in vocabulary order over the kept ids (sampling.rs:302-328)
+  float ev[kLargePer], pre2[kLargePer];
+  bool kept[kLargePer];
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) {
+    const uint32_t j = kLargePer * t + q;
+    kept[q] = j < n_c && S.candv[j] <= last_kept;
+    ev[q] = kept[q] ? expf_glibc(val_of(S.candv[j]) - vmax) : 0.0f;
+  }
+  const float S2 = small_seq_prefix(ev, pre2, S);
+  float pv[kLargePer];
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) pv[q] = kept[q] ? ev[q] / S2 : 0.0f;
+  small_seq_prefix(pv, pre2, S);
+  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+  uint32_t first = 0xffffffffu;
+  if (u > 0.0f) {
+#pragma unroll
+    for (int q = kLargePer - 1; q >= 0; --q)
+      if (kept[q] && pre2[q] >= u) first = kLargePer * t + q;
+  }
+  first = block_min_u(first, S.s);
+  const uint32_t tok = (u > 0.0f && first != 0xffffffffu) ? (uint32_t)S.candv[first] : 0u;
+  finish_row(a, row, tok, TC_OK, flags);
+  put_norm(a, row, S2);
+  if (a.topk_count) {
+    // survivors and kept ids in vocabulary order
+    uint32_t cs = 0, ck = 0;
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t j = kLargePer * t + q;
+      cs += (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) ? 1u : 0u;
+      ck += kept[q] ? 1u : 0u;
+    }
+    uint32_t ts, tk;
+    uint32_t os = block_excl_scan(cs, S.s, &ts);
+    uint32_t ok = block_excl_scan(ck, S.s, &tk);
+#pragma unroll
+    for (int q = 0; q < kLargePer; ++q) {
+      const uint32_t j = kLargePer * t + q;
+      if (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) {
+        if (os < a.cap) a.topk_ids[(size_t)row * a.cap + os] = (uint32_t)S.candv[j];
+        ++os;
+      }
+      if (kept[q]) {
+        if (ok < a.cap) {
+          a.keep_ids[(size_t)row * a.cap + ok] = (uint32_t)S.candv[j];
+          a.keep_probs[(size_t)row * a.cap + ok] = pv[q];
+        }
+        ++ok;
+      }
+    }
+    if (t == 0) {
+      a.topk_count[row] = ts;
+      a.keep_count[row] = tk;
+    }
+  }
+}
+
+// indextts with the typical warper (generation.rs:649-651, off by default):
+// the general path with idx_typical between the penalty and the temperature.
+template <typename InT, int ITEMS>
+__global__ void __launch_bounds__(max_threads(ITEMS)) k_idx_typical(RowArgs a) {
+  __shared__ IdxGenLds G;
+  idx_general<InT, ITEMS, true>(a, G);
 }
 
 __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
@@ -2150,7 +2327,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   }
   // Rows the streaming passes below do not decide -- non-finite logits, a
   // negative penalty, a K-th key more than 256 keys below the largest, a K-th
-  // logit overflowing to -inf -- get their candidates from large_general,
+  // logit overflowing to -inf -- get their candidates from large_candidates,
   // which streams the row again from memory; the common rows keep the row
   // tiles in registers throughout.
   const uint32_t K = (uint32_t)a.K;
@@ -2202,7 +2379,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
   const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
   if (bad || bK == 0xffffffffu || (a.do_pen && a.pen_f < 0.0f) || thr == -__builtin_inff()) {
-    n_c = large_general(a, S, base, nchunks, shift, eos, kmax, bad ? 0xffffffffu : bK, bad != 0u, &row_flags);
+    n_c = large_candidates<uint16_t>(a, S, row, eos, &row_flags);
     if (n_c == 0xffffffffu) {  // a +inf logit: the reference's CDF is NaN -> index 0
       finish_row(a, row, 0u, TC_OK, row_flags);
       no_verify(a, row);
@@ -2294,119 +2471,78 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       parity ^= 1;
     });
   }
+  large_finish(a, S, row, n_c, row_flags);
+}
+
+// qwen at large vocabularies for what k_qwen_large's packed bf16 passes do not
+// take: f32 rows, the penalty mask (TC_HIST_MASK) and the additive mask.
+// Greedy rows take candle's argmax over the final logits (the first index of
+// the largest, NaN skipped, a NaN at index 0 never replaced); the others
+// stream their candidates (large_candidates) and share k_qwen_large's finish.
+template <typename InT>
+__global__ void __launch_bounds__(kLargeThreads) k_qwen_large_gen(RowArgs a) {
+  __shared__ QLargeLds S;
+  const int row = blockIdx.x, t = threadIdx.x, V = a.V;
+  const int eos = (a.eos_id >= 0 && a.eos_id < V) ? a.eos_id : -1;
+  const int nwords = (V + 31) >> 5;
+  const bool use_bits = a.do_pen && a.hist_mode != TC_HIST_MASK;
+  if (use_bits) {
+    for (int w = t; w < nwords; w += blockDim.x) S.bits[w] = 0u;
+    __syncthreads();
+    uint32_t h0, h1;
+    hist_range(a, row, &h0, &h1);
+    for (uint32_t k = h0 + (uint32_t)t; k < h1; k += blockDim.x) {
+      const uint32_t id = a.hist_ids[k];
+      if (id < (uint32_t)V) atomicOr(&S.bits[id >> 5], 1u << (id & 31u));
+    }
+  }
   __syncthreads();
-  if (n_c > (uint32_t)kLargeCand) {
-    finish_row(a, row, 0u, TC_EUNSUPPORTED, row_flags);
+  if (a.greedy) {
+    constexpr int E = LargeRow<InT>::kEpc;
+    const LargeRow<InT> R(a, row);
+    uint64_t best = 0;
+    uint32_t bad = 0;
+    for (int q = t; q < R.nchunks; q += blockDim.x) {
+      const uint4 v = R.base[q];
+      const int c0 = q * E - R.shift;
+      const uint32_t hb = use_bits ? bits_at_fn(S.bits, nwords, c0) : 0u;
+#pragma unroll
+      for (int h = 0; h < E; ++h) {
+        const int e = c0 + h;
+        if (e < 0 || e >= V) continue;
+        const float lv = qlogit_all(a, chunk_val<InT>(v, h), ((hb >> h) & 1u) != 0u, e, eos);
+        if (__builtin_isnan(lv)) {
+          bad |= e == 0 ? 2u : 1u;
+          continue;
+        }
+        const uint64_t k = ((uint64_t)ckey(lv) << 32) | (uint64_t)(~(uint32_t)e);
+        best = k > best ? k : best;
+      }
+    }
+    bad = block_or_u(bad, S.s);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const uint64_t other = __shfl_xor(best, o);
+      best = other > best ? other : best;
+    }
+    if (lane_id() == 0) S.cand[wave_id()] = best;
+    __syncthreads();
+    if (t == 0) {
+      uint64_t b = 0;
+      for (int w = 0; w < num_waves(); ++w) b = S.cand[w] > b ? S.cand[w] : b;
+      finish_row(a, row, (b && !(bad & 2u)) ? ~(uint32_t)(b & 0xffffffffu) : 0u, TC_OK, TC_FLAG_GREEDY);
+    }
     no_verify(a, row);
     return;
   }
-  // rank order: more than 256 candidates sort as 2048 keys in registers
-  const int n_pad = n_c > 256u ? kLargeCand : next_pow2((int)n_c < 2 ? 2 : (int)n_c);
-  for (int j = (int)n_c + t; j < n_pad; j += blockDim.x) S.cand[j] = ~0ull;
-  __syncthreads();
-  if (n_pad == kLargeCand) block_sort2048(S.cand);
-  else block_bitonic_sort(S.cand, n_pad);
-  // top-k (sampling.rs:224-249): every value >= the K-th largest
-  const uint32_t kth_hi = (uint32_t)(S.cand[K - 1] >> 32);  // ~ckey of the K-th value
-  auto val_of = [](uint64_t kv) { return untkey(~(uint32_t)(kv >> 32)); };
-  uint32_t ns_part = 0;
-  for (int j = t; j < (int)n_c; j += blockDim.x) ns_part += (uint32_t)(S.cand[j] >> 32) <= kth_hi ? 1u : 0u;
-  const uint32_t ns = block_sum_u(ns_part, S.s);
-  const float vmax = val_of(S.cand[0]);
-  if (vmax == __builtin_inff()) {  // a finite value overflowing to +inf: as above
+  uint32_t row_flags = 0;
+  const uint32_t n_c = large_candidates<InT>(a, S, row, eos, &row_flags);
+  if (n_c == 0xffffffffu) {  // a +inf logit: the reference's CDF is NaN -> index 0
     finish_row(a, row, 0u, TC_OK, row_flags);
     no_verify(a, row);
     return;
   }
-  uint32_t flags = row_flags, cut = ns;
-  if (a.do_topp) {
-    // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential
-    // sum, running sum of e / S, cutoff at the first crossing (kept)
-    float e[kLargePer], pre[kLargePer];
-#pragma unroll
-    for (int q = 0; q < kLargePer; ++q) {
-      const uint32_t r = kLargePer * t + q;
-      e[q] = r < ns ? expf_glibc(val_of(S.cand[r]) - vmax) : 0.0f;
-    }
-    float Sr = small_seq_prefix(e, pre, S);
-    float pq[kLargePer];
-#pragma unroll
-    for (int q = 0; q < kLargePer; ++q) pq[q] = (kLargePer * t + q) < ns ? e[q] / Sr : 0.0f;
-    small_seq_prefix(pq, pre, S);
-    uint32_t first = 0xffffffffu;
-#pragma unroll
-    for (int q = kLargePer - 1; q >= 0; --q)
-      if ((kLargePer * t + q) < ns && pre[q] > a.top_p_f) first = kLargePer * t + q;
-    first = block_min_u(first, S.s);
-    if (first != 0xffffffffu) cut = first + 1;
-    if (cut < ns && (uint32_t)(S.cand[cut - 1] >> 32) == (uint32_t)(S.cand[cut] >> 32)) flags |= TC_FLAG_TIE_CUT;
-  }
-  const uint64_t last_kept = S.cand[cut - 1];
-  // softmax + multinomial in vocabulary order over the kept ids (sampling.rs:302-328)
-  float ev[kLargePer], pre2[kLargePer];
-  bool kept[kLargePer];
-#pragma unroll
-  for (int q = 0; q < kLargePer; ++q) {
-    const uint32_t j = kLargePer * t + q;
-    kept[q] = j < n_c && S.candv[j] <= last_kept;
-    ev[q] = kept[q] ? expf_glibc(val_of(S.candv[j]) - vmax) : 0.0f;
-  }
-  const float S2 = small_seq_prefix(ev, pre2, S);
-  float pv[kLargePer];
-#pragma unroll
-  for (int q = 0; q < kLargePer; ++q) pv[q] = kept[q] ? ev[q] / S2 : 0.0f;
-  small_seq_prefix(pv, pre2, S);
-  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
-  uint32_t first = 0xffffffffu;
-  if (u > 0.0f) {
-#pragma unroll
-    for (int q = kLargePer - 1; q >= 0; --q)
-      if (kept[q] && pre2[q] >= u) first = kLargePer * t + q;
-  }
-  first = block_min_u(first, S.s);
-  const uint32_t tok = (u > 0.0f && first != 0xffffffffu) ? (uint32_t)S.candv[first] : 0u;
-  finish_row(a, row, tok, TC_OK, flags);
-  put_norm(a, row, S2);
-  if (a.topk_count) {
-    // survivors and kept ids in vocabulary order
-    uint32_t cs = 0, ck = 0;
-#pragma unroll
-    for (int q = 0; q < kLargePer; ++q) {
-      const uint32_t j = kLargePer * t + q;
-      cs += (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) ? 1u : 0u;
-      ck += kept[q] ? 1u : 0u;
-    }
-    uint32_t ts, tk;
-    uint32_t os = block_excl_scan(cs, S.s, &ts);
-    uint32_t ok = block_excl_scan(ck, S.s, &tk);
-#pragma unroll
-    for (int q = 0; q < kLargePer; ++q) {
-      const uint32_t j = kLargePer * t + q;
-      if (j < n_c && (uint32_t)(S.candv[j] >> 32) <= kth_hi) {
-        if (os < a.cap) a.topk_ids[(size_t)row * a.cap + os] = (uint32_t)S.candv[j];
-        ++os;
-      }
-      if (kept[q]) {
-        if (ok < a.cap) {
-          a.keep_ids[(size_t)row * a.cap + ok] = (uint32_t)S.candv[j];
-          a.keep_probs[(size_t)row * a.cap + ok] = pv[q];
-        }
-        ++ok;
-      }
-    }
-    if (t == 0) {
-      a.topk_count[row] = ts;
-      a.keep_count[row] = tk;
-    }
-  }
-}
-
-// indextts with the typical warper (generation.rs:649-651, off by default):
-// the general path with idx_typical between the penalty and the temperature.
-template <typename InT, int ITEMS>
-__global__ void __launch_bounds__(max_threads(ITEMS)) k_idx_typical(RowArgs a) {
-  __shared__ IdxGenLds G;
-  idx_general<InT, ITEMS, true>(a, G);
+  large_finish(a, S, row, n_c, row_flags);
 }
 
 // ================================================================ cosyvoice3
@@ -4094,11 +4230,18 @@ static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, 
     if (p->variant == TC_QWEN && a.do_pen && (a.pen_f == 0.0f || !isfinite(a.pen_f)))
       return fail(TC_EUNSUPPORTED, "tc_sample: repetition penalty %g above %d logits", p->repetition_penalty,
                   tc::kMaxVocabReg);
-    if (p->variant == TC_QWEN && dtype == TC_BF16 && V <= tc::kLargeVocab && p->hist_mode != TC_HIST_MASK &&
-        !p->d_add_mask && (a.K >= 1 || a.greedy) && a.K <= tc::kLargeCand) {
+    if (p->variant == TC_QWEN && V <= tc::kLargeVocab && (a.K >= 1 || a.greedy) && a.K <= tc::kLargeCand) {
+      // bf16 rows without masks: the packed passes; f32 rows and the masks:
+      // candidates selected on the final logits
       DeviceGuard g(device);
-      hipLaunchKernelGGL(tc::k_qwen_large, dim3((unsigned)rows), dim3(tc::kLargeThreads), 0,
-                         reinterpret_cast<hipStream_t>(stream), a);
+      hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+      const dim3 gr((unsigned)rows), bl(tc::kLargeThreads);
+      if (dtype == TC_BF16 && p->hist_mode != TC_HIST_MASK && !p->d_add_mask)
+        hipLaunchKernelGGL(tc::k_qwen_large, gr, bl, 0, st, a);
+      else if (dtype == TC_BF16)
+        hipLaunchKernelGGL(tc::k_qwen_large_gen<uint16_t>, gr, bl, 0, st, a);
+      else
+        hipLaunchKernelGGL(tc::k_qwen_large_gen<float>, gr, bl, 0, st, a);
       hipError_t e = hipGetLastError();
       return e == hipSuccess ? TC_OK : hip_fail(e, "tc_sample launch");
     }

@@ -765,3 +765,65 @@ def test_qwen_large_vocab_overflow(sampler):
     assert g["status"][3] == 0
     tie = (o["flags"] & 1) != 0
     same(g, o, rows=[r for r in (3,) if not tie[r]])
+
+
+@pytest.mark.parametrize("V", [16500, 151936])
+def test_qwen_large_vocab_f32_rows(sampler, V):
+    # f32 rows above the register-resident size: candidates selected on the
+    # final logits (k_qwen_large_gen), the same finish as the bf16 kernel
+    g_ = np.random.default_rng(V + 3)
+    rows = 4
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    x[1] -= np.float32(10.0)                              # shifted row
+    x[2, g_.integers(0, V, 3)] = np.float32(40.0)         # peaked row
+    hist = [g_.integers(0, V, 400).tolist() for _ in range(rows)]
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.7, top_k=1000, top_p=0.95, penalty=1.1),
+               dict(temperature=1.0, top_k=50, top_p=0.8, penalty=-1.5, eos_id=11),
+               dict(temperature=0.9, top_k=7, top_p=1.0, penalty=1.0)):
+        print(f"[large f32] V={V} {kw}", flush=True)
+        g, o = run(sampler, O.QWEN, x, hist, u, ld_pad=1, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_qwen_large_vocab_masks(sampler, bf16):
+    # the talker's chain at a large vocabulary: penalty mask (TC_HIST_MASK),
+    # suppression mask, EOS, temperature; and greedy over the same
+    V, rows = 151936, 3
+    g_ = np.random.default_rng(91 + bf16)
+    x = (g_.standard_normal((rows, V)) * 3).astype(np.float32)
+    eos = V - 7
+    supp = np.zeros(V, np.float32)
+    supp[V - 1024:] = -np.inf
+    supp[eos] = 0.0
+    pm = np.zeros(V, np.float32)
+    pm[g_.integers(0, V, 3000)] = 1.0
+    pm[np.argsort(-x[0])[:20]] = 1.0                      # penalise some of the top ids
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.9, top_k=50, top_p=0.9, penalty=1.3, eos_id=eos),
+               dict(temperature=0.7, top_k=300, top_p=0.8, penalty=0.8),
+               dict(temperature=0.005, top_k=50, top_p=0.9, penalty=1.3)):
+        print(f"[large masks] bf16={bf16} {kw}", flush=True)
+        g, o = run(sampler, O.QWEN, x, None, u, bf16=bf16, hist_mode=2, add_mask=supp, pen_mask=pm, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+def test_qwen_large_vocab_f32_non_finite(sampler):
+    V = 151936
+    g_ = np.random.default_rng(95)
+    x = (g_.standard_normal((3, V)) * 3).astype(np.float32)
+    x[0, 777] = np.inf                       # +inf -> index 0
+    x[1, g_.integers(0, V, 4000)] = -np.inf  # -inf entries weigh zero
+    x[2, 9] = np.nan                         # NaN left out, row flagged
+    g, o = run(sampler, O.QWEN, x, [[1], [2], [3]], g_.random(3), temperature=0.8, top_k=100, top_p=0.9,
+               penalty=1.2)
+    assert (g["status"] == 0).all(), g["status"]
+    assert g["ids"][0] == 0 and o["ids"][0] == 0
+    tie = (o["flags"] & 1) != 0
+    same(g, o, rows=[1] if not tie[1] else [])
+    assert g["flags"][2] & _lib.FLAG_NAN_ROW and g["ids"][2] != 9
