@@ -657,53 +657,54 @@ __device__ __forceinline__ bool qwen_fast(const RowArgs& a, QFastLds& F) {
 
 // ================================================================ qwen, top-p over many survivors
 // The general path's LDS: the history map and the survivor stage, or, past
-// them, the rank sort of up to kWideCap survivors.
-constexpr int kWideCap = 4096;
+// them, the rank keys of every survivor of a register-resident row.
+constexpr int kWideCap = kMaxVocabReg;
 struct QGenLds {
   uint8_t seen[kMaxVocabReg];
   SurvLds sv;
 };
+// The fast path's LDS shares the union: it hands a row over only after its
+// last access.  Kept under 80 KB, so two workgroups fit a CU.
 union QGenU {
   QGenLds g;
-  uint64_t wide[kWideCap];
+  uint32_t wide[kWideCap];  // ~ckey of each survivor's value: ascending = value descending
+  QFastLds f;
 };
-static_assert(sizeof(uint64_t) * kWideCap <= sizeof(QGenLds), "the rank sort fits the general path's LDS");
 
-// top-p (sampling.rs:255-299) over kSurvCap < n <= kWideCap survivors (top-k
-// off or wide), then softmax and the draw (302-328) by qwen_wide_cdf over the
-// kept ones.  Every survivor is sorted into rank order (value descending, id
-// ascending; the reference's unstable sort leaves ties open: TC_FLAG_TIE_CUT
-// where they straddle the cut); thread t then holds ranks ITEMS * t + i (n <=
-// V <= ITEMS * blockDim), so the sequential f32 denominator in rank order and
-// the running sum of e / S are block_seqsum and seq_prefix over those
-// positions; the cut follows the first running sum above p (the crossing
-// rank kept).
+// top-p (sampling.rs:255-299) over more than kSurvCap survivors (top-k off or
+// wide), then softmax and the draw (302-328) by qwen_wide_cdf over the kept
+// ones.  The survivors' values are sorted into rank order (value descending;
+// equal values are equal terms, so the sums need no ids); thread t then holds
+// ranks ITEMS * t + i (n <= V <= ITEMS * blockDim), the sequential f32
+// denominator in rank order and the running sum of e / S are block_seqsum
+// and seq_prefix over those positions, and the cut follows the first running
+// sum above p (the crossing rank kept).  The kept ids are the values above
+// the cut's, and of the values equal to it the lowest ids, as many as the
+// cut leaves (the reference's unstable sort leaves that order open:
+// TC_FLAG_TIE_CUT where equal values straddle the cut).
 template <int ITEMS>
 __device__ __forceinline__ void qwen_wide_topp(const RowArgs& a, const float (&x)[ITEMS], uint32_t surv, uint32_t vm,
                                                int e0, uint32_t n, uint32_t flags, QGenU& U, BlockScratch& s,
                                                uint32_t* s_out, SeqLds& sq, ScanLds& sc) {
   const int t = threadIdx.x;
-  // the survivors' rank keys, compacted in vocabulary order, padded, sorted
+  // the survivors' rank keys, padded, sorted
   uint32_t tot;
   uint32_t pos = block_excl_scan((uint32_t)__builtin_popcount(surv), s, &tot);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i)
-    if ((surv >> i) & 1u) U.wide[pos++] = ((uint64_t)(~ckey(x[i])) << 32) | (uint32_t)(e0 + i);
+    if ((surv >> i) & 1u) U.wide[pos++] = ~ckey(x[i]);
   const int n_pad = next_pow2((int)n < 2 ? 2 : (int)n);
-  for (int j = (int)n + t; j < n_pad; j += blockDim.x) U.wide[j] = ~0ull;
+  for (int j = (int)n + t; j < n_pad; j += blockDim.x) U.wide[j] = 0xffffffffu;
   __syncthreads();
   block_bitonic_sort(U.wide, n_pad);
   // ranks ITEMS * t + i in registers
   const int p0 = ITEMS * t;
   float v[ITEMS], e[ITEMS];
-  uint32_t id[ITEMS];
-  const float vmax = untkey(~(uint32_t)(U.wide[0] >> 32));
+  const float vmax = untkey(~U.wide[0]);
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     const bool in = p0 + i < (int)n;
-    const uint64_t kv = in ? U.wide[p0 + i] : 0ull;
-    v[i] = in ? untkey(~(uint32_t)(kv >> 32)) : 0.0f;
-    id[i] = (uint32_t)kv;
+    v[i] = in ? untkey(~U.wide[p0 + i]) : 0.0f;
     e[i] = in ? expf_glibc(v[i] - vmax) : 0.0f;
   }
   __syncthreads();  // the sort buffer is free from here
@@ -713,7 +714,7 @@ __device__ __forceinline__ void qwen_wide_topp(const RowArgs& a, const float (&x
   {
     SeqThread<ITEMS> th;
     if (!block_seqsum<ITEMS>(e, ~0u, e, same, p0, 0, th, sq, sc, &S))
-      S = block_seqsum_slow<ITEMS>(e, p0, (int)n, stage, kWideCap * 2, &sq.S);
+      S = block_seqsum_slow<ITEMS>(e, p0, (int)n, stage, kWideCap, &sq.S);
   }
   float q[ITEMS];
 #pragma unroll
@@ -753,42 +754,51 @@ __device__ __forceinline__ void qwen_wide_topp(const RowArgs& a, const float (&x
     }
   }
   const uint32_t cut = first != 0xffffffffu ? first + 1u : n;
-  // equal values straddling the cut: the reference's unstable order decides
+  // the values at ranks cut - 1 and cut (equal: a tie straddles the cut)
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
     if ((uint32_t)(p0 + i) + 1u == cut) s_out[2] = f2u(v[i]);
     if ((uint32_t)(p0 + i) == cut) s_out[3] = f2u(v[i]);
   }
-  // the kept ids (ranks below the cut) as a bitmap over the vocabulary
-  uint32_t* bm = reinterpret_cast<uint32_t*>(U.wide);
-  const int nwords = (a.V + 31) >> 5;
-  for (int w = t; w < nwords; w += blockDim.x) bm[w] = 0u;
   __syncthreads();
+  const float vcut = u2f(s_out[2]);
   if (cut < n && s_out[2] == s_out[3]) flags |= TC_FLAG_TIE_CUT;
+  // kept: values above vcut, and the first (cut - above) ids, in vocabulary
+  // order, of those equal to it
+  uint32_t above = 0, eq = 0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i)
-    if ((uint32_t)(p0 + i) < cut) atomicOr(&bm[id[i] >> 5], 1u << (id[i] & 31u));
-  __syncthreads();
+    if ((surv >> i) & 1u) {
+      above += x[i] > vcut ? 1u : 0u;
+      eq += x[i] == vcut ? 1u : 0u;
+    }
+  const uint32_t n_above = block_sum_u(above, s);
+  uint32_t eq_tot;
+  uint32_t eq_rank = block_excl_scan(eq, s, &eq_tot);
+  const uint32_t keep_eq = cut - n_above;
   uint32_t kept = 0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    const int el = e0 + i;
-    if (((surv >> i) & 1u) && ((bm[el >> 5] >> (el & 31)) & 1u)) kept |= 1u << i;
+    if (!((surv >> i) & 1u)) continue;
+    if (x[i] > vcut) kept |= 1u << i;
+    else if (x[i] == vcut) {
+      if (eq_rank < keep_eq) kept |= 1u << i;
+      ++eq_rank;
+    }
   }
-  __syncthreads();  // the bitmap shares LDS with the CDF's staging
+  __syncthreads();  // the sort buffer shares LDS with the CDF's staging
   qwen_wide_cdf<ITEMS>(a, x, kept, surv, vm, e0, cut, flags, U.g.sv, s, sq, sc);
 }
 
 // ================================================================ qwen
 template <typename InT, int ITEMS>
 __global__ void __launch_bounds__(max_threads(ITEMS)) k_qwen(RowArgs a) {
+  __shared__ QGenU U;
   if (a.fast) {
-    __shared__ QFastLds qf;
-    if (qwen_fast<InT, ITEMS>(a, qf)) return;
+    if (qwen_fast<InT, ITEMS>(a, U.f)) return;
     __syncthreads();
   }
-  __shared__ QGenU U;
   uint8_t* s_seen = U.g.seen;
   SurvLds& sv = U.g.sv;
   __shared__ uint32_t s_hist[256];

@@ -436,7 +436,8 @@ __device__ __forceinline__ bool block_kth_largest(const uint32_t (&key)[ITEMS], 
 // two stages that both stay inside segments the wave orders its own LDS
 // accesses (one wave's LDS operations complete in order; the fences keep the
 // compiler from moving them); any other boundary takes a block barrier.
-__device__ __forceinline__ void block_bitonic_sort(uint64_t* a, int n_pad) {
+template <typename KeyT>
+__device__ __forceinline__ void block_bitonic_sort(KeyT* a, int n_pad) {
   const int half = n_pad >> 1;
   const bool segs = (blockDim.x & 63u) == 0u;
   for (int k = 2; k <= n_pad; k <<= 1) {
@@ -444,7 +445,7 @@ __device__ __forceinline__ void block_bitonic_sort(uint64_t* a, int n_pad) {
       for (int p = threadIdx.x; p < half; p += blockDim.x) {
         const int i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
         const int ixj = i + j;
-        const uint64_t x = a[i], y = a[ixj];
+        const KeyT x = a[i], y = a[ixj];
         const bool up = (i & k) == 0;
         if ((x > y) == up) {
           a[i] = y;
