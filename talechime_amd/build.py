@@ -6,7 +6,8 @@ Steps:
   1. compile and run csrc/gen_expf_table.c (host, gcc) to produce
      csrc/_gen/expf_glibc_exc.inc and csrc/_gen/logf_glibc_exc.inc -- skipped
      when both includes are newer than the generator and tc_math.h;
-  2. hipcc --offload-arch=gfx950 -shared the kernels and the C ABI into
+  2. hipcc --offload-arch=gfx950 -c each kernel source (in parallel, one
+     process per file) and -shared the objects into
      talechime_amd/libtalechime_hip.so;
   3. the same for csrc/selftest.hip into talechime_amd/libtc_selftest.so
      (on-device checks of the approximations, loaded by the tests only).
@@ -35,7 +36,6 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
@@ -75,11 +75,26 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
+# The library's sources: the C ABI with the small kernels and the beam steps
+# (sampler.hip), one file per sampler family, and the LM head.
+LIB_SRCS = ["sampler.hip", "k_qwen.hip", "k_indextts.hip", "k_idx_typical.hip", "k_large.hip", "k_cosy.hip", "k_moss.hip", "lm_head.hip"]
+OBJ = os.path.join(CSRC, "_gen", "obj")
+
+
 def build_lib() -> str:
-    srcs = [os.path.join(CSRC, "sampler.hip"), os.path.join(CSRC, "lm_head.hip")]
+    os.makedirs(OBJ, exist_ok=True)
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
+    jobs = []
+    for name in LIB_SRCS:
+        obj = os.path.join(OBJ, name.replace(".hip", ".o"))
+        cmd = [hipcc(), *HIPCC_FLAGS, *inc, "-c", os.path.join(CSRC, name), "-o", obj]
+        jobs.append((name, obj, subprocess.Popen(cmd)))
+    failed = [name for name, _, pr in jobs if pr.wait() != 0]
+    if failed:
+        raise RuntimeError("hipcc failed on " + ", ".join(failed))
     out_tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, *srcs, "-o", out_tmp]
-    subprocess.run(cmd, check=True)
+    subprocess.run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *[o for _, o, _ in jobs], "-o", out_tmp],
+                   check=True)
     os.replace(out_tmp, LIB)
     return LIB
 
@@ -87,7 +102,7 @@ def build_lib() -> str:
 def build_selftest() -> str:
     """On-device checks of the approximations (tests load it; the sampler does not)."""
     out_tmp = SELFTEST + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC,
+    cmd = [hipcc(), *HIPCC_FLAGS, "-shared", "-I", os.path.join(ROOT, "include"), "-I", CSRC,
            os.path.join(CSRC, "selftest.hip"), "-o", out_tmp]
     subprocess.run(cmd, check=True)
     os.replace(out_tmp, SELFTEST)

@@ -29,7 +29,10 @@ def _check(g, o, rows):
     near = (g["flags"] & NEAR) != 0
     print(f"[typical] rows {len(rows)} near {int(near.sum())} statuses {np.unique(g['status'])}", flush=True)
     assert near.sum() == 0
-    same(g, o, rows=[r for r in rows if not near[r]])
+    # rows with more than 1024 survivors: probabilities from block sums
+    wide = o["topk_count"] > 1024
+    same(g, o, rows=[r for r in rows if not near[r] and not wide[r]])
+    same(g, o, rows=[r for r in rows if not near[r] and wide[r]], probs_exact=False)
 
 
 @pytest.mark.parametrize("mass", [0.9, 0.5, 0.2])
@@ -45,9 +48,8 @@ def test_typical_workload_rows(sampler, mass):
 
 @pytest.mark.parametrize("scale", [0.5, 2.0, 6.0])
 def test_typical_alone_and_peaked_rows(sampler, scale):
-    # no top-k / top-p: the kept set is the typical set itself; rows whose
-    # set exceeds the survivor stage report TC_EUNSUPPORTED, as the oracle's
-    # count says
+    # no top-k / top-p: the kept set is the typical set itself, also where it
+    # exceeds the survivor stage (the register-resident path)
     g_ = np.random.default_rng(int(scale * 10))
     V, rows = 8194, 24
     x = (g_.standard_normal((rows, V)) * scale).astype(np.float32)
@@ -55,9 +57,9 @@ def test_typical_alone_and_peaked_rows(sampler, scale):
     hist = [g_.integers(0, V, 40).tolist() for _ in range(rows)]
     g, o = run(sampler, O.INDEXTTS, x, hist, g_.random(rows), temperature=1.0, top_k=0, top_p=1.0, penalty=1.3,
                min_keep=2, typical=True, typical_mass=0.6)
-    big = o["topk_count"] > 1024
-    assert (g["status"][big] == _lib.TC_EUNSUPPORTED).all()
-    _check(g, o, [r for r in range(rows) if not big[r]])
+    if scale < 1.0:
+        assert (o["topk_count"] > 1024).all()
+    _check(g, o, range(rows))
 
 
 def test_typical_small_rows_ties_and_infinities(sampler):
