@@ -152,6 +152,9 @@ def pool_parity(w, logits, hists, hoff, unis, sampler, params, n_batches):
 
     from oracle import oracle as O
 
+    if n_batches <= 0:
+        return None
+
     p = O.make_params(w.variant, temperature=w.temperature, top_k=w.top_k, top_p=w.top_p,
                       penalty=w.penalty, min_keep=w.min_keep, ras_win=w.ras_win, ras_tau=w.ras_tau)
     threads = host_cpus()[0]
