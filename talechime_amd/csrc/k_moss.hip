@@ -55,13 +55,12 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
   block_rank_keys<ITEMS>(key, surv, K, true, U.wide, s, rk);
   const float maximum = untkey(~U.wide[0]);
   const int p0 = ITEMS * t;
-  float wf[ITEMS];
+  // the weight at rank position p0 + i, recomputed where needed (fewer live
+  // registers than holding it)
+  auto wfv = [&](int i) { return p0 + i < (int)K ? expf_glibc((untkey(~opaque(rk[i])) - maximum) / a.t_f) : 0.0f; };
   double part = 0.0;
 #pragma unroll
-  for (int i = 0; i < ITEMS; ++i) {
-    wf[i] = p0 + i < (int)K ? expf_glibc((untkey(~rk[i]) - maximum) / a.t_f) : 0.0f;
-    part += (double)wf[i];
-  }
+  for (int i = 0; i < ITEMS; ++i) part += (double)wfv(i);
   double T;
   const double W0 = block_excl_scan_d(part, sc, &T);
   // keep: the first rank whose running sum of w / total exceeds top_p, plus one
@@ -69,7 +68,7 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
   double W = W0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    W += (double)wf[i];
+    W += (double)wfv(i);
     le += (p0 + i < (int)K && !(W / T > a.top_p_d)) ? 1u : 0u;
   }
   const uint32_t n_le = block_sum_u(le, s);
@@ -78,7 +77,7 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
   W = W0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    W += (double)wf[i];
+    W += (double)wfv(i);
     const uint32_t p = (uint32_t)(p0 + i);
     if (p < K && (p + 1u == n_le || p == n_le) && !settled(W / T, a.top_p_d, K)) near = 1;
     if (p + 1u == keep) *s_sw = W;  // the kept weights' sum
@@ -92,7 +91,7 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
   W = W0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    W += (double)wf[i];
+    W += (double)wfv(i);
     lt += ((uint32_t)(p0 + i) < keep && W < usw) ? 1u : 0u;
   }
   const uint32_t n_lt = block_sum_u(lt, s);
@@ -101,7 +100,7 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
   uint32_t near2 = 0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    W += (double)wf[i];
+    W += (double)wfv(i);
     const uint32_t p = (uint32_t)(p0 + i);
     if (p < keep && (p + 1u == n_lt || p == n_lt) && !settled(W, usw, K)) near2 = 1;
   }
@@ -113,7 +112,7 @@ __device__ __forceinline__ void moss_wide(const RowArgs& a, const float (&x)[ITE
     float* wr = reinterpret_cast<float*>(U.wide);
 #pragma unroll
     for (int i = 0; i < ITEMS; ++i)
-      if (p0 + i < (int)K) wr[p0 + i] = wf[i];
+      if (p0 + i < (int)K) wr[p0 + i] = wfv(i);
     __syncthreads();
     if (t == 0) {
       double total = -0.0;
@@ -324,7 +323,7 @@ __device__ __forceinline__ void nano_wide(const RowArgs& a, const float (&x)[ITE
   uint32_t key[ITEMS];
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) key[i] = tkey(x[i]);
-  auto wv = [&](float v) { return tc_exp_d((double)(v - maximum)); };
+  auto wv = [&](float v) { return tc_exp_d((double)(opaque(v) - maximum)); };
   uint32_t pos = 0, inexact = 0;  // survivors with a positive weight; one not exp(0)
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i)

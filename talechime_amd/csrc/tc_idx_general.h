@@ -364,7 +364,7 @@ __device__ __forceinline__ void idx_wide(const RowArgs& a, const float (&x)[ITEM
       c = floor_keep;
     } else if (!nan_any) {
       const int p0 = ITEMS * t;
-      auto wt = [&](int i) { return p0 + i < (int)n ? tc_exp_d((double)untkey(rk[i]) - md) : 0.0; };
+      auto wt = [&](int i) { return p0 + i < (int)n ? tc_exp_d((double)untkey(opaque(rk[i])) - md) : 0.0; };
       double part = 0.0;
 #pragma unroll
       for (int i = 0; i < ITEMS; ++i) part += wt(i);
@@ -395,7 +395,7 @@ __device__ __forceinline__ void idx_wide(const RowArgs& a, const float (&x)[ITEM
         // the reference's loops: the denominator in vocabulary order, then
         // the running sum in rank order up to its first value above lim
         const VocabPos<ITEMS> vp = vocab_pos<ITEMS>(surv, s);
-        auto wx = [&](int i) { return tc_exp_d((double)x[i] - md); };
+        auto wx = [&](int i) { return tc_exp_d((double)opaque(x[i]) - md); };
         double Sq = -0.0;
         staged_walk<ITEMS>(n, vp, wx, stage, WL, [&](uint32_t, double v) {
           Sq += v;
@@ -463,7 +463,7 @@ __device__ __forceinline__ void idx_wide(const RowArgs& a, const float (&x)[ITEM
   for (int i = 0; i < ITEMS; ++i)
     if ((live >> i) & 1u) ml = rmaxd(ml, (double)x[i] + 0.0);
   ml = block_max_d(ml, s);
-  auto ew = [&](int i) { return ((live >> i) & 1u) ? tc_exp_d(((double)x[i] + 0.0) - ml) : 0.0; };
+  auto ew = [&](int i) { return ((live >> i) & 1u) ? tc_exp_d(((double)opaque(x[i]) + 0.0) - ml) : 0.0; };
   double part = 0.0;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) part += ew(i);

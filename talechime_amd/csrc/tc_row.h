@@ -188,6 +188,18 @@ __device__ __forceinline__ void no_verify(const RowArgs& a, int row) {
 // the rank order comes from their 32-bit keys sorted in LDS, where equal
 // values are equal terms, so the order-dependent sums need no ids.
 
+// A copy of v the compiler cannot see through: a weight recomputed from it at
+// each use stays a recomputation, instead of one value per item held live in
+// registers across the row's passes (which spills the wide shapes).
+__device__ __forceinline__ float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // The survivor stage, or the sorted keys of every survivor of the row.
 union SurvWide {
   SurvLds sv;
