@@ -11,12 +11,16 @@
 // the kernel streams the weights once per group of rows with 16-byte loads
 // and accumulates in f32 on the VALU.
 //
-// k_lm_head: one wave per block of kHeadVB vocabulary rows; lane l takes the
-// 16-byte chunks l, l + 64, ... of each weight row (kHeadCPL of them at most),
-// all issued before the first product; the group's hidden rows (<= kHeadRG)
-// are staged in LDS once per workgroup; each lane keeps kHeadVB x rows partial
+// k_lm_head_reg (up to 4 rows, the decode case): one wave per block of
+// kHeadVB vocabulary rows; lane l takes the 16-byte chunks l, l + 64, ... of
+// each weight row and the matching slices of the hidden rows, loaded first so
+// that they are in when the weights arrive; no LDS and no barrier.
+// k_lm_head (more rows): the same weight layout held in registers while the
+// hidden rows pass through LDS kHeadRG8 at a time, so the weights are read
+// once whatever the number of rows.  Each lane keeps kHeadVB x rows partial
 // dot products, reduced across the wave with DPP at the end.  Logit = that
-// dot product + bias (candle's Linear: matmul, then broadcast add).
+// dot product + bias (candle's Linear: matmul, then broadcast add), the bias
+// loaded with the weights.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -27,9 +31,9 @@
 namespace tc {
 
 constexpr int kHeadVB = 4;      // vocabulary rows per wave
-constexpr int kHeadRG = 4;      // hidden rows per pass (16 for larger batches when they fit LDS)
-constexpr int kHeadRG8 = 8, kHeadRG16 = 16;
-constexpr size_t kHeadLds = 64 * 1024;  // dynamic LDS a launch may take without an attribute
+constexpr int kHeadRG = 4;      // hidden rows per LDS chunk when 8 do not fit
+constexpr int kHeadRG8 = 8;     // hidden rows per LDS chunk
+constexpr size_t kHeadLds = 64 * 1024;  // dynamic LDS per workgroup at most
 constexpr int kHeadCPL = 8;     // 16-byte weight chunks per lane at most (bf16: dim <= 4096)
 constexpr int kHeadWaves = 4;   // waves per workgroup
 constexpr int kHeadMaxDim = 4096;
@@ -60,8 +64,11 @@ __global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head(HeadArgs a) {
   constexpr int kEpc = sizeof(WT) == 2 ? 8 : 4;  // elements per 16-byte chunk
   const int nchunk = a.dim / kEpc;
   const int v0 = (blockIdx.x * kHeadWaves + wave) * kHeadVB;
-  // every weight chunk of the wave's rows, issued first so that HBM works
-  // while the hidden rows are staged
+  // the wave's bias values and every weight chunk of its rows, issued first
+  // so that HBM works while the hidden rows are staged
+  float bsv[kHeadVB];
+#pragma unroll
+  for (int b = 0; b < kHeadVB; ++b) bsv[b] = a.bias ? a.bias[min(v0 + b, a.vocab - 1)] : 0.0f;
   uint4 w[kHeadVB][CPL];
 #pragma unroll
   for (int b = 0; b < kHeadVB; ++b) {
@@ -73,17 +80,119 @@ __global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head(HeadArgs a) {
       w[b][j] = (c < nchunk && v0 < a.vocab) ? row[c] : make_uint4(0u, 0u, 0u, 0u);
     }
   }
-  // the pass's hidden rows into LDS, 16 bytes at a time (rows past a.rows
-  // read as zeros; dim is a multiple of 4)
+  // the rows RG at a time through LDS while the weights stay in registers:
+  // HBM reads the weights once whatever the number of rows (rows past
+  // a.rows read as zeros; dim is a multiple of 4)
   const int q4 = a.dim >> 2;
-  for (int i = threadIdx.x; i < RG * q4; i += blockDim.x) {
-    const int r = i / q4, k = i - r * q4;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (r < a.rows) v = reinterpret_cast<const float4*>(a.hidden + (size_t)r * (size_t)a.hid_ld)[k];
-    reinterpret_cast<float4*>(hs)[i] = v;
+  for (int r0 = 0; r0 < a.rows; r0 += RG) {
+    for (int i = threadIdx.x; i < RG * q4; i += blockDim.x) {
+      const int r = i / q4, k = i - r * q4;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (r0 + r < a.rows) v = reinterpret_cast<const float4*>(a.hidden + (size_t)(r0 + r) * (size_t)a.hid_ld)[k];
+      reinterpret_cast<float4*>(hs)[i] = v;
+    }
+    __syncthreads();
+    if (v0 < a.vocab) {
+      float acc[kHeadVB][RG];
+#pragma unroll
+      for (int b = 0; b < kHeadVB; ++b)
+#pragma unroll
+        for (int r = 0; r < RG; ++r) acc[b][r] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane + 64 * j;
+        if (c >= nchunk) break;
+        // the chunk's weights widened once, then one pass over the hidden rows
+        float wf[kHeadVB][8];
+#pragma unroll
+        for (int b = 0; b < kHeadVB; ++b) {
+          const uint4 q = w[b][j];
+          if (kEpc == 8) {
+            wf[b][0] = bf16_lo(q.x); wf[b][1] = bf16_hi(q.x); wf[b][2] = bf16_lo(q.y); wf[b][3] = bf16_hi(q.y);
+            wf[b][4] = bf16_lo(q.z); wf[b][5] = bf16_hi(q.z); wf[b][6] = bf16_lo(q.w); wf[b][7] = bf16_hi(q.w);
+          } else {
+            wf[b][0] = __uint_as_float(q.x); wf[b][1] = __uint_as_float(q.y);
+            wf[b][2] = __uint_as_float(q.z); wf[b][3] = __uint_as_float(q.w);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          float h[8];
+          const float4* hp = reinterpret_cast<const float4*>(&hs[r * a.dim + c * kEpc]);
+          const float4 h0 = hp[0];
+          h[0] = h0.x; h[1] = h0.y; h[2] = h0.z; h[3] = h0.w;
+          if (kEpc == 8) {
+            const float4 h1 = hp[1];
+            h[4] = h1.x; h[5] = h1.y; h[6] = h1.z; h[7] = h1.w;
+          }
+#pragma unroll
+          for (int b = 0; b < kHeadVB; ++b) {
+            float s = acc[b][r];
+#pragma unroll
+            for (int e = 0; e < kEpc; ++e) s = __builtin_fmaf(wf[b][e], h[e], s);
+            acc[b][r] = s;
+          }
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < kHeadVB; ++b) {
+        const int v = v0 + b;
+#pragma unroll
+        for (int r = 0; r < RG; ++r) {
+          const float t = dpp_wave_sum(acc[b][r]);
+          if (lane == 0 && v < a.vocab && r0 + r < a.rows)
+            a.logits[(size_t)(r0 + r) * (size_t)a.out_ld + v] = a.bias ? t + bsv[b] : t;
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with this chunk's rows
   }
-  __syncthreads();
+}
+
+// Decode sizes (rows per pass x chunks per lane <= kHeadRegSlices): no LDS and
+// no barrier.  Each lane loads the slices of the hidden rows its chunks meet
+// (chunk c covers elements kEpc c .. kEpc c + kEpc - 1 of every row), then
+// every weight chunk of the wave's rows, chunk by chunk: the loads return in
+// issue order, so the products of chunk j start as soon as its weights are in
+// while the later chunks are still on their way.  The hidden rows come from
+// L2 after the first waves read them.
+constexpr int kHeadRegSlices = 12;
+template <typename WT, int CPL, int RG>
+__global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head_reg(HeadArgs a) {
+  static_assert(CPL * RG <= kHeadRegSlices, "hidden slices held per lane");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int kEpc = sizeof(WT) == 2 ? 8 : 4;  // elements per 16-byte chunk
+  constexpr int kHq = kEpc / 4;                   // float4 of hidden values per chunk
+  const int nchunk = a.dim / kEpc;
+  const int v0 = (blockIdx.x * kHeadWaves + wave) * kHeadVB;
   if (v0 >= a.vocab) return;
+  // the wave's bias values, in flight with everything else
+  float bsv[kHeadVB];
+#pragma unroll
+  for (int b = 0; b < kHeadVB; ++b) bsv[b] = a.bias ? a.bias[min(v0 + b, a.vocab - 1)] : 0.0f;
+  float4 hv[CPL][RG][kHq];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) {
+      const float4* hp = reinterpret_cast<const float4*>(a.hidden + (size_t)r * (size_t)a.hid_ld) + c * kHq;
+#pragma unroll
+      for (int q = 0; q < kHq; ++q)
+        hv[j][r][q] = (c < nchunk && r < a.rows) ? hp[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+  uint4 w[CPL][kHeadVB];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+#pragma unroll
+    for (int b = 0; b < kHeadVB; ++b) {
+      const int v = min(v0 + b, a.vocab - 1);
+      const uint4* row = reinterpret_cast<const uint4*>(reinterpret_cast<const WT*>(a.weight) + (size_t)v * (size_t)a.dim);
+      w[j][b] = c < nchunk ? row[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
   float acc[kHeadVB][RG];
 #pragma unroll
   for (int b = 0; b < kHeadVB; ++b)
@@ -91,21 +200,17 @@ __global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head(HeadArgs a) {
     for (int r = 0; r < RG; ++r) acc[b][r] = 0.0f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = lane + 64 * j;
-    if (c >= nchunk) break;
+    if (lane + 64 * j >= nchunk) break;
 #pragma unroll
     for (int r = 0; r < RG; ++r) {
       float h[8];
-      const float4* hp = reinterpret_cast<const float4*>(&hs[r * a.dim + c * kEpc]);
-      const float4 h0 = hp[0];
-      h[0] = h0.x; h[1] = h0.y; h[2] = h0.z; h[3] = h0.w;
+      h[0] = hv[j][r][0].x; h[1] = hv[j][r][0].y; h[2] = hv[j][r][0].z; h[3] = hv[j][r][0].w;
       if (kEpc == 8) {
-        const float4 h1 = hp[1];
-        h[4] = h1.x; h[5] = h1.y; h[6] = h1.z; h[7] = h1.w;
+        h[4] = hv[j][r][kHq - 1].x; h[5] = hv[j][r][kHq - 1].y; h[6] = hv[j][r][kHq - 1].z; h[7] = hv[j][r][kHq - 1].w;
       }
 #pragma unroll
       for (int b = 0; b < kHeadVB; ++b) {
-        const uint4 q = w[b][j];
+        const uint4 q = w[j][b];
         float s = acc[b][r];
         if (kEpc == 8) {
           s = __builtin_fmaf(bf16_lo(q.x), h[0], s);
@@ -133,7 +238,7 @@ __global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head(HeadArgs a) {
     for (int r = 0; r < RG; ++r) {
       const float t = dpp_wave_sum(acc[b][r]);
       if (lane == 0 && v < a.vocab && r < a.rows)
-        a.logits[(size_t)r * (size_t)a.out_ld + v] = a.bias ? t + a.bias[v] : t;
+        a.logits[(size_t)r * (size_t)a.out_ld + v] = a.bias ? t + bsv[b] : t;
     }
   }
 }
@@ -143,19 +248,45 @@ __global__ void __launch_bounds__(kHeadWaves * 64) k_lm_head(HeadArgs a) {
 namespace {
 int head_fail(int code, const char* msg) { return tc::set_error(code, msg); }
 
+// The register kernel for rg rows per pass (1..4) and cpl chunks per lane,
+// when rg x cpl fits its hidden slices; false otherwise.
+template <typename WT, int RG>
+bool launch_head_reg_rg(int cpl, unsigned blocks, hipStream_t st, const tc::HeadArgs& a, hipError_t* e) {
+  const dim3 g(blocks), b(tc::kHeadWaves * 64);
+  constexpr int kMax = tc::kHeadRegSlices / RG;
+  if (cpl <= 1) hipLaunchKernelGGL((tc::k_lm_head_reg<WT, 1, RG>), g, b, 0, st, a);
+  else if (cpl <= 2 && kMax >= 2) hipLaunchKernelGGL((tc::k_lm_head_reg<WT, (kMax >= 2 ? 2 : 1), RG>), g, b, 0, st, a);
+  else if (cpl <= 3 && kMax >= 3) hipLaunchKernelGGL((tc::k_lm_head_reg<WT, (kMax >= 3 ? 3 : 1), RG>), g, b, 0, st, a);
+  else if (cpl <= 4 && kMax >= 4) hipLaunchKernelGGL((tc::k_lm_head_reg<WT, (kMax >= 4 ? 4 : 1), RG>), g, b, 0, st, a);
+  else if (cpl <= 8 && kMax >= 8) hipLaunchKernelGGL((tc::k_lm_head_reg<WT, (kMax >= 8 ? 8 : 1), RG>), g, b, 0, st, a);
+  else return false;
+  *e = hipGetLastError();
+  return true;
+}
+template <typename WT>
+bool launch_head_reg(int rows, int cpl, unsigned blocks, hipStream_t st, const tc::HeadArgs& a, hipError_t* e) {
+  if (rows <= 1) return launch_head_reg_rg<WT, 1>(cpl, blocks, st, a, e);
+  if (rows <= 2) return launch_head_reg_rg<WT, 2>(cpl, blocks, st, a, e);
+  if (rows <= 3) return launch_head_reg_rg<WT, 3>(cpl, blocks, st, a, e);
+  if (rows <= 4) return launch_head_reg_rg<WT, 4>(cpl, blocks, st, a, e);
+  return false;
+}
+
+template <typename WT, int CPL, int RG>
+hipError_t launch_head_k(unsigned blocks, size_t lds, hipStream_t st, const tc::HeadArgs& a) {
+  hipLaunchKernelGGL((tc::k_lm_head<WT, CPL, RG>), dim3(blocks), dim3(tc::kHeadWaves * 64), lds, st, a);
+  return hipGetLastError();
+}
 template <typename WT, int RG>
 hipError_t launch_head_rg(int cpl, unsigned blocks, size_t lds, hipStream_t st, const tc::HeadArgs& a) {
-  const dim3 g(blocks), b(tc::kHeadWaves * 64);
-  if (cpl <= 1) hipLaunchKernelGGL((tc::k_lm_head<WT, 1, RG>), g, b, lds, st, a);
-  else if (cpl <= 2) hipLaunchKernelGGL((tc::k_lm_head<WT, 2, RG>), g, b, lds, st, a);
-  else if (cpl <= 3) hipLaunchKernelGGL((tc::k_lm_head<WT, 3, RG>), g, b, lds, st, a);
-  else if (cpl <= 4) hipLaunchKernelGGL((tc::k_lm_head<WT, 4, RG>), g, b, lds, st, a);
-  else hipLaunchKernelGGL((tc::k_lm_head<WT, 8, RG>), g, b, lds, st, a);
-  return hipGetLastError();
+  if (cpl <= 1) return launch_head_k<WT, 1, RG>(blocks, lds, st, a);
+  if (cpl <= 2) return launch_head_k<WT, 2, RG>(blocks, lds, st, a);
+  if (cpl <= 3) return launch_head_k<WT, 3, RG>(blocks, lds, st, a);
+  if (cpl <= 4) return launch_head_k<WT, 4, RG>(blocks, lds, st, a);
+  return launch_head_k<WT, 8, RG>(blocks, lds, st, a);
 }
 template <typename WT>
 hipError_t launch_head(int rg, int cpl, unsigned blocks, size_t lds, hipStream_t st, const tc::HeadArgs& a) {
-  if (rg == tc::kHeadRG16) return launch_head_rg<WT, tc::kHeadRG16>(cpl, blocks, lds, st, a);
   if (rg == tc::kHeadRG8) return launch_head_rg<WT, tc::kHeadRG8>(cpl, blocks, lds, st, a);
   return launch_head_rg<WT, tc::kHeadRG>(cpl, blocks, lds, st, a);
 }
@@ -180,26 +311,47 @@ int tc_lm_head(const float* d_hidden, size_t hidden_ld, const void* d_weight, in
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)((vocab + tc::kHeadVB * tc::kHeadWaves - 1) / (tc::kHeadVB * tc::kHeadWaves));
   const int cpl = (int)((dim / epc + 63) / 64);
-  // passes of 16 or 8 rows when their hidden states fit LDS, else of 4
-  auto fits = [&](int g) { return (size_t)g * dim * sizeof(float) <= tc::kHeadLds; };
-  const int rg = rows <= (size_t)tc::kHeadRG ? tc::kHeadRG
-                 : (fits(tc::kHeadRG16) ? tc::kHeadRG16 : (fits(tc::kHeadRG8) ? tc::kHeadRG8 : tc::kHeadRG));
-  const size_t lds = (size_t)rg * dim * sizeof(float);
-  for (size_t r0 = 0; r0 < rows; r0 += (size_t)rg) {
-    tc::HeadArgs a{};
-    a.hidden = d_hidden + r0 * hidden_ld;
-    a.hid_ld = (long long)hidden_ld;
-    a.weight = d_weight;
-    a.bias = d_bias;
-    a.logits = d_logits + r0 * logits_ld;
-    a.out_ld = (long long)logits_ld;
-    a.rows = (int)(rows - r0 < (size_t)rg ? rows - r0 : (size_t)rg);
-    a.dim = (int)dim;
-    a.vocab = (int)vocab;
-    const hipError_t e = w_dtype == TC_BF16 ? launch_head<uint16_t>(rg, cpl, blocks, lds, st, a)
-                                            : launch_head<float>(rg, cpl, blocks, lds, st, a);
-    if (e != hipSuccess) return head_fail(TC_EHIP, hipGetErrorString(e));
+  // the register kernel when every row fits its hidden slices in one pass
+  // (up to 4 rows); more rows take the LDS kernel, whose passes hold 8 or 16
+  const int cpl_t = cpl <= 4 ? cpl : 8;  // the kernels' chunk counts: 1, 2, 3, 4, 8
+  const int reg_rg = tc::kHeadRegSlices / cpl_t < 4 ? tc::kHeadRegSlices / cpl_t : 4;
+  if (reg_rg >= 1 && rows <= (size_t)reg_rg) {
+    for (size_t r0 = 0; r0 < rows; r0 += (size_t)reg_rg) {
+      tc::HeadArgs a{};
+      a.hidden = d_hidden + r0 * hidden_ld;
+      a.hid_ld = (long long)hidden_ld;
+      a.weight = d_weight;
+      a.bias = d_bias;
+      a.logits = d_logits + r0 * logits_ld;
+      a.out_ld = (long long)logits_ld;
+      a.rows = (int)(rows - r0 < (size_t)reg_rg ? rows - r0 : (size_t)reg_rg);
+      a.dim = (int)dim;
+      a.vocab = (int)vocab;
+      hipError_t e = hipSuccess;
+      const bool ok = w_dtype == TC_BF16 ? launch_head_reg<uint16_t>(a.rows, cpl, blocks, st, a, &e)
+                                         : launch_head_reg<float>(a.rows, cpl, blocks, st, a, &e);
+      if (!ok) return head_fail(TC_EHIP, "tc_lm_head: no register kernel for this shape");
+      if (e != hipSuccess) return head_fail(TC_EHIP, hipGetErrorString(e));
+    }
+    return TC_OK;
   }
+  // one launch for every row: the kernel takes them 8 (or, past the LDS, 4)
+  // at a time through LDS with the weights held in registers
+  const int rg = (size_t)tc::kHeadRG8 * dim * sizeof(float) <= tc::kHeadLds ? tc::kHeadRG8 : tc::kHeadRG;
+  const size_t lds = (size_t)rg * dim * sizeof(float);
+  tc::HeadArgs a{};
+  a.hidden = d_hidden;
+  a.hid_ld = (long long)hidden_ld;
+  a.weight = d_weight;
+  a.bias = d_bias;
+  a.logits = d_logits;
+  a.out_ld = (long long)logits_ld;
+  a.rows = (int)rows;
+  a.dim = (int)dim;
+  a.vocab = (int)vocab;
+  const hipError_t e = w_dtype == TC_BF16 ? launch_head<uint16_t>(rg, cpl, blocks, lds, st, a)
+                                          : launch_head<float>(rg, cpl, blocks, lds, st, a);
+  if (e != hipSuccess) return head_fail(TC_EHIP, hipGetErrorString(e));
   return TC_OK;
 }
 

@@ -39,11 +39,14 @@ def _case(rows, dim, vocab, wdt, bias, seed):
 
 
 @pytest.mark.parametrize("rows,dim,vocab,wdt,bias", [
-    (3, 1280, 8194, "bf16", True),     # indextts mel_head, one element x 3 beams
+    (3, 1280, 8194, "bf16", True),     # indextts mel_head, one element x 3 beams (register kernel)
     (1, 1280, 8194, "f32", True),
-    (16, 1024, 2048, "bf16", False),   # code predictor lm_head, 16 rows (4 passes)
+    (2, 1280, 8194, "bf16", False),
+    (4, 1024, 2048, "bf16", True),
+    (16, 1024, 2048, "bf16", False),   # code predictor lm_head, 16 rows (two LDS chunks of 8)
     (5, 2048, 3072, "f32", False),
-    (7, 4096, 1000, "bf16", True),
+    (7, 4096, 1000, "bf16", True),     # chunks of 4 rows (8 do not fit the LDS)
+    (61, 1280, 8194, "bf16", True),    # 8 chunks, the last partial
 ])
 def test_lm_head_within_rounding_of_exact_product(sampler, rows, dim, vocab, wdt, bias):
     h, w, b, wt = _case(rows, dim, vocab, wdt, bias, rows * 1000 + dim)
