@@ -153,11 +153,15 @@ __device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, ui
     v[q] = u2f((uint32_t)(cv >> 32));
     id[q] = (uint32_t)cv;
     key[q] = has[q] ? (((uint64_t)ckey(v[q]) << 32) | (uint64_t)(~c)) : 0ull;
-    if (q < NS) F.rkey[c] = key[q];
   }
-  lds_wait();
+  const uint32_t K = (uint32_t)a.K;
   uint32_t rk[2] = {0u, 0u};
-  {
+  float kth;
+  if (a.do_topp) {
+    // ranks (value descending, id ascending) for the rank-order sums
+#pragma unroll
+    for (int q = 0; q < NS; ++q) F.rkey[q * kWave + lane] = key[q];
+    lds_wait();
     const uint32_t nr = (n + 3u) & ~3u;
     for (uint32_t j = 0; j < nr; j += 4) {
       const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1], k2 = F.rkey[j + 2], k3 = F.rkey[j + 3];
@@ -165,11 +169,27 @@ __device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, ui
       for (int q = 0; q < NS; ++q)
         rk[q] += ((k0 > key[q] ? 1u : 0u) + (k1 > key[q] ? 1u : 0u)) + ((k2 > key[q] ? 1u : 0u) + (k3 > key[q] ? 1u : 0u));
     }
+    // top-k (224-249): keep v >= the K-th largest, ties kept
+    const uint64_t bk0 = __ballot(has[0] && rk[0] == K - 1u), bk1 = __ballot(has[1] && rk[1] == K - 1u);
+    kth = bk0 ? rl_f32(v[0], __builtin_ctzll(bk0)) : rl_f32(v[1], __builtin_ctzll(bk1));
+  } else {
+    // without top-p only the K-th largest value is needed: the largest
+    // 32-bit key T with at least K keys >= T, bit by bit over wave ballots
+    // (at least K candidates are staged, so it exists)
+    uint32_t k32[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) k32[q] = has[q] ? (uint32_t)(key[q] >> 32) : 0u;
+    uint32_t T = 0;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = T | (1u << b);
+      uint32_t cnt = (uint32_t)__popcll(__ballot(k32[0] >= c));
+      if (NS == 2) cnt += (uint32_t)__popcll(__ballot(k32[1] >= c));
+      T = cnt >= K ? c : T;
+    }
+    const uint64_t e0 = __ballot(k32[0] == T), e1 = __ballot(k32[1] == T);
+    kth = e0 ? rl_f32(v[0], __builtin_ctzll(e0)) : rl_f32(v[1], __builtin_ctzll(e1));
   }
-  // top-k (224-249): keep v >= the K-th largest, ties kept
-  const uint32_t K = (uint32_t)a.K;
-  const uint64_t bk0 = __ballot(has[0] && rk[0] == K - 1u), bk1 = __ballot(has[1] && rk[1] == K - 1u);
-  const float kth = bk0 ? rl_f32(v[0], __builtin_ctzll(bk0)) : rl_f32(v[1], __builtin_ctzll(bk1));
   bool surv[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) surv[q] = has[q] && v[q] >= kth;
@@ -224,7 +244,7 @@ __device__ __forceinline__ void qwen_fast_finish_t(const RowArgs& a, int row, ui
     if (ok) {
       bool kp[2];
 #pragma unroll
-      for (int q = 0; q < 2; ++q) kp[q] = surv[q] && rk[q] < cut;
+      for (int q = 0; q < 2; ++q) kp[q] = surv[q] && (!a.do_topp || rk[q] < cut);
       const float S2t = dpp_wave_sum((kp[0] ? e[0] : 0.0f) + (kp[1] ? e[1] : 0.0f));
       const uint64_t km0 = __ballot(kp[0]), km1 = __ballot(kp[1]);
       const uint32_t nk = (uint32_t)(__popcll(km0) + __popcll(km1));
