@@ -314,8 +314,11 @@ union CosyLds {
 // sequential f32 sums over at most top_k ranks, and the repetition window
 // (llm.rs:532-536).  C.out[0] = the nucleus token, C.out[1] = 1 when the
 // window fired (the row then draws from random_sample_probs instead).
+// wid: lane j's id of the repetition window (the last ras_win decoded ids),
+// loaded at the start of the row when the window fits a wave; else unused.
 template <int NS>
-__device__ __forceinline__ void cosy_fast_finish_t(const RowArgs& a, int row, uint32_t n, float S, CosyFastLds& C) {
+__device__ __forceinline__ void cosy_fast_finish_t(const RowArgs& a, int row, uint32_t n, float S, CosyFastLds& C,
+                                                   uint32_t wid) {
   FinLds& F = C.fin;
   const int lane = lane_id();
   float p[2];
@@ -335,18 +338,19 @@ __device__ __forceinline__ void cosy_fast_finish_t(const RowArgs& a, int row, ui
     if (q < NS) F.rkey[c] = key[q];
   }
   lds_wait();
-  // rank = number of candidates with a larger key
+  // rank = number of candidates with a larger key (zero keys pad the slots
+  // past n up to a multiple of 4)
   uint32_t rk[2] = {0u, 0u};
   {
     const uint32_t nr = (n + 3u) & ~3u;
     uint32_t a0 = 0, a1 = 0, b0 = 0, b1 = 0;
-    for (uint32_t j = 0; j < nr; j += 2) {
-      const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1];
-      a0 += k0 > key[0] ? 1u : 0u;
-      a1 += k1 > key[0] ? 1u : 0u;
+    for (uint32_t j = 0; j < nr; j += 4) {
+      const uint64_t k0 = F.rkey[j], k1 = F.rkey[j + 1], k2 = F.rkey[j + 2], k3 = F.rkey[j + 3];
+      a0 += (k0 > key[0] ? 1u : 0u) + (k1 > key[0] ? 1u : 0u);
+      a1 += (k2 > key[0] ? 1u : 0u) + (k3 > key[0] ? 1u : 0u);
       if (NS == 2) {
-        b0 += k0 > key[1] ? 1u : 0u;
-        b1 += k1 > key[1] ? 1u : 0u;
+        b0 += (k0 > key[1] ? 1u : 0u) + (k1 > key[1] ? 1u : 0u);
+        b1 += (k2 > key[1] ? 1u : 0u) + (k3 > key[1] ? 1u : 0u);
       }
     }
     rk[0] = has[0] ? a0 + a1 : 0xffffffffu;
@@ -362,10 +366,84 @@ __device__ __forceinline__ void cosy_fast_finish_t(const RowArgs& a, int row, ui
       *ir = rl_u32(id[1], __builtin_ctzll(m1));
     }
   };
+  // The nucleus loop, its total and the draw add the same terms in the same
+  // (rank) order from zero, so one running sum cum_r decides all three: the
+  // kept count nc (the first r <= kmax - 2 with cum_r >= top_p, plus one;
+  // else kmax), total = cum_{nc-1}, and the token at the first r < nc with
+  // u total < cum_r.  Without verification outputs they are first decided
+  // from a wave scan of the probabilities by rank, which stays within
+  // (n + 32) 2^-22 of the sequential sums; a decision inside that margin runs
+  // the reference's loops below.
+  const uint32_t kmax = (uint32_t)a.top_k < n ? (uint32_t)a.top_k : n;
+  if (!a.topk_count && kmax >= 1u) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      if (has[q]) {
+        F.wr32[rk[q]] = p[q];
+        F.k32[rk[q]] = id[q];
+      }
+    lds_wait();
+    float pr[2], c[2];
+    float carry = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t r = (uint32_t)(q * kWave + lane);
+      pr[q] = (q < NS && r < n) ? F.wr32[r] : 0.0f;
+      c[q] = q < NS ? dpp_scan_f32(pr[q]) + carry : 0.0f;
+      if (q < NS) carry = rl_f32(c[q], kWave - 1);
+    }
+    auto cum_at = [&](uint32_t r) { return rl_f32(r < 64u ? c[0] : c[1], (int)(r & 63u)); };
+    const float mg = (float)(n + 32u) * 0x1p-22f;
+    const float tp = a.top_p_f;
+    // the crossing among ranks 0 .. kmax - 2
+    const uint32_t lim = kmax - 1u;
+    const uint64_t x0 = __ballot((uint32_t)lane < lim && c[0] >= tp);
+    const uint64_t x1 = __ballot((uint32_t)(kWave + lane) < lim && c[1] >= tp);
+    const uint32_t rx = x0 ? (uint32_t)__builtin_ctzll(x0) : (x1 ? 64u + (uint32_t)__builtin_ctzll(x1) : lim);
+    bool ok = true;
+    uint32_t nc2;
+    if (rx < lim) {
+      nc2 = rx + 1u;
+      ok = cum_at(rx) - tp > mg && (rx == 0u || tp - cum_at(rx - 1u) > mg);
+    } else {
+      nc2 = kmax;
+      ok = lim == 0u || tp - cum_at(lim - 1u) > mg;
+    }
+    if (ok) {
+      const float total = cum_at(nc2 - 1u);
+      const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row] * total;
+      const uint64_t d0 = __ballot((uint32_t)lane < nc2 && c[0] > pick);
+      const uint64_t d1 = __ballot((uint32_t)(kWave + lane) < nc2 && c[1] > pick);
+      const uint32_t rd = d0 ? (uint32_t)__builtin_ctzll(d0) : (d1 ? 64u + (uint32_t)__builtin_ctzll(d1) : nc2);
+      // pick carries the total's uncertainty (mg, scaled by u <= 1) and its
+      // own rounding
+      const float mgd = 2.0f * mg + pick * 0x1p-23f;
+      ok = rd < nc2 && cum_at(rd) - pick > mgd && (rd == 0u || pick - cum_at(rd - 1u) > mgd);
+      if (ok) {
+        const uint32_t tk = F.k32[rd];
+        uint32_t rep = 0;
+        if (a.ras_win <= kWave) {
+          rep = (uint32_t)__popcll(__ballot(wid == tk));
+        } else {
+          uint32_t h0, h1;
+          hist_range(a, row, &h0, &h1);
+          const uint32_t w0 = (h1 - h0) > (uint32_t)a.ras_win ? h1 - (uint32_t)a.ras_win : h0;
+          for (uint32_t j = w0 + (uint32_t)lane; j < h1; j += (uint32_t)kWave) rep += a.hist_ids[j] == tk ? 1u : 0u;
+          rep = rl_u32(dpp_scan_u32(rep), kWave - 1);
+        }
+        const bool ras = (float)rep >= a.ras_thresh;
+        if (lane == 0) {
+          if (!ras) put_result(a, row, tk, TC_OK, 0u);
+          C.out[0] = tk;
+          C.out[1] = ras ? 1u : 0u;
+        }
+        return;
+      }
+    }
+  }
   // while cum < top_p and len < top_k: cum += p (the crossing token is kept)
   float cum = 0.0f;
   uint32_t nc = 0;
-  const uint32_t kmax = (uint32_t)a.top_k < n ? (uint32_t)a.top_k : n;
   while (nc < kmax && cum < a.top_p_f) {
     float pr;
     uint32_t ir;
@@ -400,12 +478,16 @@ __device__ __forceinline__ void cosy_fast_finish_t(const RowArgs& a, int row, ui
     }
   }
   // the repetition window: how often top occurs in the last ras_win decoded
-  uint32_t h0, h1;
-  hist_range(a, row, &h0, &h1);
-  const uint32_t w0 = (h1 - h0) > (uint32_t)a.ras_win ? h1 - (uint32_t)a.ras_win : h0;
   uint32_t rep = 0;
-  for (uint32_t j = w0 + (uint32_t)lane; j < h1; j += (uint32_t)kWave) rep += a.hist_ids[j] == top ? 1u : 0u;
-  rep = rl_u32(dpp_scan_u32(rep), kWave - 1);
+  if (a.ras_win <= kWave) {
+    rep = (uint32_t)__popcll(__ballot(wid == top));
+  } else {
+    uint32_t h0, h1;
+    hist_range(a, row, &h0, &h1);
+    const uint32_t w0 = (h1 - h0) > (uint32_t)a.ras_win ? h1 - (uint32_t)a.ras_win : h0;
+    for (uint32_t j = w0 + (uint32_t)lane; j < h1; j += (uint32_t)kWave) rep += a.hist_ids[j] == top ? 1u : 0u;
+    rep = rl_u32(dpp_scan_u32(rep), kWave - 1);
+  }
   const bool ras = (float)rep >= a.ras_thresh;
   if (lane == 0) {
     if (!ras) put_result(a, row, top, TC_OK, 0u);
@@ -456,6 +538,15 @@ __device__ __forceinline__ bool cosy_fast(const RowArgs& a, CosyLds& U) {
   float x[ITEMS];
   int shift;
   load_row<ITEMS>(rp, V, x, &shift);
+  // the repetition window's ids (the last ras_win of the history), in flight
+  // with the row for the finishing wave; 0xffffffff matches no token
+  uint32_t wid = 0xffffffffu;
+  if (wave_id() == 0 && a.ras_win <= kWave) {
+    uint32_t h0, h1;
+    hist_range(a, row, &h0, &h1);
+    const uint32_t w0 = (h1 - h0) > (uint32_t)a.ras_win ? h1 - (uint32_t)a.ras_win : h0;
+    if (w0 + (uint32_t)lane_id() < h1) wid = a.hist_ids[w0 + (uint32_t)lane_id()];
+  }
   if (t < 64) F.bins[t] = 0u;
   const int e0 = t * ITEMS - shift;
   // the ignore_eos mask (llm.rs:525-529): the EOS term is an exact zero
@@ -545,8 +636,8 @@ __device__ __forceinline__ bool cosy_fast(const RowArgs& a, CosyLds& U) {
   }
   put_norm(a, row, S);
   if (wave_id() == 0) {
-    if (n <= (uint32_t)kWave) cosy_fast_finish_t<1>(a, row, n, S, F);
-    else cosy_fast_finish_t<2>(a, row, n, S, F);
+    if (n <= (uint32_t)kWave) cosy_fast_finish_t<1>(a, row, n, S, F, wid);
+    else cosy_fast_finish_t<2>(a, row, n, S, F, wid);
   }
   __syncthreads();
   const bool ras = F.out[1] != 0u;  // the nucleus token (F.out[0]) is already written otherwise

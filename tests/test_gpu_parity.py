@@ -153,6 +153,29 @@ def test_cosy_workload_bit_exact(sampler, batch_index):
         assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
 
 
+@pytest.mark.parametrize("batch_index", [0, 1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("ras_tau", [None, 0.0])
+def test_cosy_workload_ids_without_verification(sampler, batch_index, ras_tau):
+    # without verification outputs the nucleus cut and the draw are first
+    # decided from a wave scan of the probabilities by rank (the reference's
+    # loops only inside the margin): the same ids and flags as the oracle,
+    # the repetition-window rows included (tau 0: every row's window fires)
+    w = synth.WORKLOADS["cosy-ras-128x6564"]
+    b = synth.make_batch(w, batch_index=batch_index)
+    over = {} if ras_tau is None else {"ras_tau": ras_tau}
+    logits, ho, hi, un = G.to_dev(b, w)
+    r = sampler.sample(G.params_for(w, "gpu", **over), logits, ho, hi, un, verify_cap=0)
+    torch.cuda.synchronize()
+    ids = r.ids.cpu().numpy().view(np.uint32)
+    o = G.run_oracle(w, b, CAP, **over)
+    mism = np.nonzero(ids != o["ids"])[0]
+    _report(w.name + " no-verify", batch=batch_index, rows=w.rows, id_mismatch=len(mism),
+            ras_rows=int(((o["flags"] & 2) != 0).sum()))
+    assert (r.status.cpu().numpy() == 0).all()
+    assert len(mism) == 0, mism[:10]
+    assert np.array_equal(r.flags.cpu().numpy(), o["flags"].astype(np.int32))
+
+
 @pytest.mark.parametrize("batch_index", [0, 1])
 def test_cosy_workload_every_window_fires(sampler, batch_index):
     # tau 0: the threshold is 0, so every row draws from random_sample_probs
