@@ -203,55 +203,92 @@ struct CosyFastLds {
   float wfin[kMaxWaves];
   uint32_t wcand[kMaxWaves];
   uint32_t out[4];
+  double wd[2][kMaxWaves];  // the repetition fallback's wave sums of p and of id * p
   SeqFastLds seq;
   FinLds fin;
   float walk[kWalk];  // the repetition fallback's probabilities around the crossing
 };
 
-// random_sample_probs (llm.rs:594-604) from the fast path's registers: pv,
-// the exact probabilities of the thread's ITEMS elements from e0 (0 outside
-// the row and at the EOS id).  An approximate running sum A (thread, wave and
-// block scans) is within E = (V + 64) * 2^-24 * 1.01 * total of the
-// reference's sequential one, so the first index with pick < acc lies in
-// [first i with A + E > pick, first i with A - E > pick].  The exact
-// sequential sum up to the window is SeqSum over the probabilities before it
-// (exact terms; elements from the window on count as zeros), and one lane
-// walks the window.  Returns the token, or 0xffffffff when the window or the
-// list does not fit (then the caller's general walk decides).  Every thread
-// of the block calls it.
+// random_sample_probs (llm.rs:594-604) from the fast path's registers: d,
+// the thread's ITEMS values of x - max from e0, vm their mask (outside the
+// row and the EOS id clear: probability an exact zero), S the reference's
+// softmax denominator.  The reference adds the probabilities p = expf(d) / S
+// in f32 in index order; each add rounds by at most 2^-24 of the running sum
+// after it, so its running sum acc_j lies within 2^-24 * 1.01 * Q_j of the
+// exact one P_j, Q_j = sum_{k <= j} P_k = (j + 1) P_j - sum_{m <= j} m p_m
+// (the 1.01 covers the errors carried from earlier adds, below V 2^-24 < 4e-4
+// of Q).  The window search runs on approximate probabilities q =
+// exp_approx(d) * (1 / S) in f32, within 2^-20 of p (2^-21 for exp_approx, a
+// few 2^-24 for the roundings of glibc's expf, the division and the product;
+// d < -87 counts as 0, p below 2^-125), summed per thread in f32 (ITEMS
+// terms: relative error below 2^-19.4) and across threads in f64 scans.
+// Together with the errors of the f32 partial sums inside a thread and of Q
+// (at most 2^-16.7 V P), E = 2^-24 * 1.01 * Q + 2^-16 P + 2^-50 at a thread's
+// last element bounds acc_j - P_j for each of its elements.  An element's
+// tests compare its thread-local f32 partial sum with pick - base -/+ E,
+// widened by 2^-23 of itself before rounding to f32: "acc_j may exceed pick"
+// and "acc_j exceeds pick".  The token, the first index with pick < acc, lies
+// in [lo, hi], lo the first element that may exceed, hi the first that
+// exceeds; when the two agree that is the token.  Otherwise pv gets the exact
+// probabilities (every lane active: the wave-cooperative expf), the exact
+// sequential sum up to the window is SeqSum over those before it (elements
+// from the window on count as zeros), and one lane walks the window.  Returns
+// the token, or 0xffffffff when the window or the list does not fit (then
+// the caller's general walk decides from pv).  Every thread of the block
+// calls it.
 template <int ITEMS>
-__device__ __forceinline__ uint32_t cosy_random_fast(const RowArgs& a, int row, const float (&pv)[ITEMS], int e0,
-                                                     CosyFastLds& F) {
+__device__ __forceinline__ uint32_t cosy_random_fast(const RowArgs& a, int row, const float (&d)[ITEMS], uint32_t vm,
+                                                     float S, int e0, CosyFastLds& F, float (&pv)[ITEMS]) {
   const int t = threadIdx.x, V = a.V, lane = lane_id(), wv = wave_id(), nw = num_waves();
   const float pick = reinterpret_cast<const float*>(a.uniforms)[2 * row + 1];
-  float pre[ITEMS];
-  float tp = 0.0f;
+  const float rS = 1.0f / S;
+  float q[ITEMS];
+  float tpf = 0.0f, tmf = 0.0f;
 #pragma unroll
   for (int i = 0; i < ITEMS; ++i) {
-    tp += pv[i];
-    pre[i] = tp;
+    q[i] = ((vm >> i) & 1u) && d[i] >= -87.0f ? exp_approx(d[i]) * rS : 0.0f;
+    tpf += q[i];
+    tmf += (float)i * q[i];
   }
-  const float tinc = dpp_scan_f32(tp);
-  if (lane == kWave - 1) F.wmax[wv] = tinc;
+  const double tp = (double)tpf, tm = (double)e0 * tp + (double)tmf;
+  const double ip = dpp_scan_f64(tp), im = dpp_scan_f64(tm);
+  if (lane == kWave - 1) {
+    F.wd[0][wv] = ip;
+    F.wd[1][wv] = im;
+  }
   lds_barrier();
-  float woff, wall;
-  wave_table_f32(F.wmax, &woff, &wall);
-  const float base = woff + (tinc - tp);
-  const float E = ((float)V + 64.0f) * 0x1p-24f * 1.01f * wall + 0x1p-60f;
+  double pb = 0.0, mb = 0.0;
+  {
+    const double vp = lane < nw ? F.wd[0][lane] : 0.0, vq = lane < nw ? F.wd[1][lane] : 0.0;
+    const double cp = dpp_scan_f64(vp), cm = dpp_scan_f64(vq);
+    const int w = __builtin_amdgcn_readfirstlane(wv);
+    if (w > 0) {
+      pb = rl_f64(cp, w - 1);
+      mb = rl_f64(cm, w - 1);
+    }
+  }
+  const double base = pb + (ip - tp);
+  const double A = base + tp, M = mb + im;  // at the thread's last element
+  const double Q = (double)(e0 + ITEMS) * A - M;
+  const double E = 0x1p-24 * 1.01 * Q + 0x1p-16 * A + 0x1p-50;
+  const double r = (double)pick - base;
+  const double tl = r - E, th = r + E;
+  const float fl = (float)(tl - 0x1p-23 * __builtin_fabs(tl) - 0x1p-140);  // at most tl
+  const float fh = (float)(th + 0x1p-23 * __builtin_fabs(th) + 0x1p-140);  // at least th
   uint32_t lo = 0xffffffffu, hi = 0xffffffffu;
+  float pf = 0.0f;
 #pragma unroll
-  for (int i = ITEMS - 1; i >= 0; --i) {
+  for (int i = 0; i < ITEMS; ++i) {
     const int e = e0 + i;
-    const float A = base + pre[i];
-    if (e >= 0 && e < V && A + E > pick) lo = (uint32_t)e;
-    if (e >= 0 && e < V && A - E > pick) hi = (uint32_t)e;
+    pf += q[i];
+    const bool in = e >= 0 && e < V;
+    if (lo == 0xffffffffu && in && pf > fl) lo = (uint32_t)e;
+    if (hi == 0xffffffffu && in && pf > fh) hi = (uint32_t)e;
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint32_t l2 = __shfl_xor(lo, o), h2 = __shfl_xor(hi, o);
-    lo = l2 < lo ? l2 : lo;
-    hi = h2 < hi ? h2 : hi;
-  }
+  // elements are in lane order: the wave's first is its first lane's
+  const uint64_t bl = __ballot(lo != 0xffffffffu), bh = __ballot(hi != 0xffffffffu);
+  lo = bl ? rl_u32(lo, __builtin_ctzll(bl)) : 0xffffffffu;
+  hi = bh ? rl_u32(hi, __builtin_ctzll(bh)) : 0xffffffffu;
   if (lane == 0) {
     F.wcand[wv] = lo;
     F.bins[wv] = hi;
@@ -261,7 +298,15 @@ __device__ __forceinline__ uint32_t cosy_random_fast(const RowArgs& a, int row, 
     lo = F.wcand[w] < lo ? F.wcand[w] : lo;
     hi = F.bins[w] < hi ? F.bins[w] : hi;
   }
+  // one element can be the first whose acc exceeds pick: it is the token
+  // (acc is non-decreasing; before lo it is <= pick, at hi above it)
+  if (lo != 0xffffffffu && lo == hi) return lo;
   if (lo == 0xffffffffu) return (uint32_t)(V - 1);  // no running sum can exceed pick
+#pragma unroll
+  for (int i = 0; i < ITEMS; ++i) {
+    const float e = expf_glibc_wave(((vm >> i) & 1u) ? d[i] : 0.0f);
+    pv[i] = ((vm >> i) & 1u) ? e / S : 0.0f;
+  }
   const uint32_t end = hi == 0xffffffffu ? (uint32_t)(V - 1) : hi;  // inclusive
   if (end - lo + 1u > (uint32_t)CosyFastLds::kWalk) return 0xffffffffu;
   // the exact sequential sum of the probabilities before the window
@@ -642,15 +687,9 @@ __device__ __forceinline__ bool cosy_fast(const RowArgs& a, CosyLds& U) {
   __syncthreads();
   const bool ras = F.out[1] != 0u;  // the nucleus token (F.out[0]) is already written otherwise
   if (ras) {
-    // random_sample_probs over every probability: exact terms for all (every
-    // lane active: the wave-cooperative expf)
+    // random_sample_probs over every probability
     float pv[ITEMS];
-#pragma unroll
-    for (int i = 0; i < ITEMS; ++i) {
-      const float e = expf_glibc_wave(((vm >> i) & 1u) ? d[i] : 0.0f);
-      pv[i] = ((vm >> i) & 1u) ? e / S : 0.0f;
-    }
-    uint32_t tok = cosy_random_fast<ITEMS>(a, row, pv, e0, F);
+    uint32_t tok = cosy_random_fast<ITEMS>(a, row, d, vm, S, e0, F, pv);
     if (tok == 0xffffffffu) {
       __syncthreads();  // the general path's arrays overlay the fast path's
       tok = cosy_random<ITEMS>(a, row, pv, valid_mask<ITEMS>(V, shift), e0, U.g);

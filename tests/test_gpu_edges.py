@@ -434,6 +434,32 @@ def test_cosy_fast_path_shapes(sampler, V, top_k, bf16):
     assert np.array_equal(g["flags"], o["flags"].astype(np.int32))
 
 
+def test_cosy_random_picks_on_running_sums(sampler):
+    # random_sample_probs (llm.rs:594-604) with the pick on the reference's f32
+    # running sum at an index, one ulp either side of it, at the row's total,
+    # next to 1 and at 0: draws decided at their exact boundary (tau 0: every
+    # window fires); near-uniform rows put many candidates inside any error
+    # window, peaked ones few
+    g_ = np.random.default_rng(41)
+    V, rows, eos = 6564, 36, 77
+    scale = np.where(np.arange(rows) % 4 == 3, 0.05, 3.0)
+    x = (g_.standard_normal((rows, V)) * scale[:, None]).astype(np.float32)
+    u = np.zeros(2 * rows, np.float32)
+    u[0::2] = g_.random(rows)
+    below1 = np.nextafter(np.float32(1.0), np.float32(0.0))
+    for r in range(rows):
+        row = x[r].copy()
+        row[eos] = -np.inf
+        acc = np.cumsum(O.softmax(row), dtype=np.float32)  # sequential f32 adds
+        a = acc[int(g_.integers(0, V))]
+        pick = (a, np.nextafter(a, np.float32(0.0)), np.nextafter(a, np.float32(2.0)), acc[-1], below1,
+                np.float32(0.0))[r % 6]
+        u[2 * r + 1] = min(pick, below1)
+    g, o = run(sampler, O.COSY_RAS, x, None, u, top_p=0.8, top_k=25, ras_win=10, ras_tau=0.0, eos_id=eos)
+    same(g, o)
+    assert ((g["flags"] & 2) != 0).all()
+
+
 def test_qwen_fast_path_extreme_uniforms(sampler):
     # u = 0 (token 0), u = 1 (reachable: the running sum may never reach it,
     # then token 0) and u next to 1, on the fast path with and without top-p
