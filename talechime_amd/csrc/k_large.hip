@@ -44,6 +44,7 @@ struct QLargeLds {
   uint64_t candv[kLargeCand];  // vocabulary order
   float stage[kLargeCand];
   uint32_t wtot[2][kMaxWaves];
+  double wd[2][kMaxWaves];
   SeqLds sq;
   ScanLds sc;
   BlockScratch s;
@@ -80,6 +81,91 @@ __device__ __forceinline__ float small_seq_prefix(const float (&tm)[kLargePer], 
   tot = S.stage[kLargeCand - 1];
   __syncthreads();
   return tot;
+}
+
+// The reference's draw decisions without its sums, when they are clear.  The
+// reference computes terms e_k = expf(d_k) at positions k < n (kLargePer per
+// thread, position kLargePer * t + q; zero where it has none), their
+// sequential f32 total S, p_k = e_k / S, and the first eligible position
+// whose sequential f32 running sum C_k of the p's exceeds thr (reaches it when
+// kGE).  Here the terms are exp_approx(d_k) (within 2^-20 of e_k; 0 below
+// -87, where e_k < 2^-125 and S >= 1), summed in f64 (thread, wave and block
+// scans).  The approximate total's distance dS from the reference's S comes
+// from the terms' error and S's own rounding, at most
+// 2^-24 * 1.02 * sum_k (n - k) e_k.  So
+// each p_k lies within eps = 2^-19 + 1.01 dS / S of its approximation, and
+// C_k within 2^-24 * 1.03 * Q_k of the exact running sum, Q_k the sum of the
+// running sums up to k.  The first position whose running sum may cross and
+// the first whose crossing is certain agree: that position.  No position may
+// cross: 0xffffffff.  Otherwise kUndecided.  Every thread calls it.
+constexpr uint32_t kUndecided = 0xfffffffeu;
+template <bool kGE>
+__device__ __forceinline__ uint32_t certified_first(const float (&d)[kLargePer], uint32_t live, uint32_t elig, int n,
+                                                    float thr, QLargeLds& S) {
+  const int t = threadIdx.x, lane = lane_id(), wv = wave_id(), nw = num_waves();
+  float ea[kLargePer];
+  double tp = 0.0, tm = 0.0;
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) {
+    ea[q] = ((live >> q) & 1u) && d[q] >= -87.0f ? exp_approx(d[q]) : 0.0f;
+    tp += (double)ea[q];
+    tm += (double)(kLargePer * t + q) * (double)ea[q];
+  }
+  const double ip = dpp_scan_f64(tp), im = dpp_scan_f64(tm);
+  if (lane == kWave - 1) {
+    S.wd[0][wv] = ip;
+    S.wd[1][wv] = im;
+  }
+  __syncthreads();
+  double pb = 0.0, mb = 0.0, Sh, Mh;
+  {
+    const double vp = lane < nw ? S.wd[0][lane] : 0.0, vq = lane < nw ? S.wd[1][lane] : 0.0;
+    const double cp = dpp_scan_f64(vp), cm = dpp_scan_f64(vq);
+    const int w = __builtin_amdgcn_readfirstlane(wv);
+    if (w > 0) {
+      pb = rl_f64(cp, w - 1);
+      mb = rl_f64(cm, w - 1);
+    }
+    Sh = rl_f64(cp, kWave - 1);
+    Mh = rl_f64(cm, kWave - 1);
+  }
+  const double dS = 0x1p-20 * Sh + 0x1p-24 * 1.02 * ((double)n * Sh - Mh) + 0x1p-40 * Sh;
+  const bool ok = Sh >= 1.0;  // the largest term is expf(0) = 1
+  const double inv = ok ? 1.0 / Sh : 0.0, eps = 0x1p-19 + 1.01 * dS * inv;
+  double A = pb + (ip - tp), M = mb + (im - tm);
+  uint32_t lo = 0xffffffffu, hi = 0xffffffffu;
+#pragma unroll
+  for (int q = 0; q < kLargePer; ++q) {
+    const int k = kLargePer * t + q;
+    A += (double)ea[q];
+    M += (double)k * (double)ea[q];
+    const double P = A * inv, Q = ((double)(k + 1) * A - M) * inv;
+    const double E = (eps + 0x1p-40) * P + 0x1p-24 * 1.03 * Q + 0x1p-60;
+    const bool e = (elig >> q) & 1u;
+    const bool may = kGE ? P + E >= (double)thr : P + E > (double)thr;
+    const bool cert = kGE ? P - E >= (double)thr : P - E > (double)thr;
+    if (lo == 0xffffffffu && e && may) lo = (uint32_t)k;
+    if (hi == 0xffffffffu && e && cert) hi = (uint32_t)k;
+  }
+  // positions are in lane order: the wave's first is its first lane's
+  // (read with every lane active)
+  const uint64_t bl = __ballot(lo != 0xffffffffu), bh = __ballot(hi != 0xffffffffu);
+  const uint32_t wl = bl ? rl_u32(lo, __builtin_ctzll(bl)) : 0xffffffffu;
+  const uint32_t wh = bh ? rl_u32(hi, __builtin_ctzll(bh)) : 0xffffffffu;
+  if (lane == 0) {
+    S.wtot[0][wv] = wl;
+    S.wtot[1][wv] = wh;
+  }
+  __syncthreads();
+  lo = hi = 0xffffffffu;
+  for (int w = 0; w < nw; ++w) {
+    lo = S.wtot[0][w] < lo ? S.wtot[0][w] : lo;
+    hi = S.wtot[1][w] < hi ? S.wtot[1][w] : hi;
+  }
+  __syncthreads();  // S.wtot and S.wd are free again
+  if (!ok) return kUndecided;
+  if (lo == 0xffffffffu) return 0xffffffffu;
+  return lo == hi ? lo : kUndecided;
 }
 
 // Bits [p, p + 32) of an LDS bitmap of nwords words (p may be negative; bits
@@ -322,10 +408,11 @@ __device__ __forceinline__ uint32_t large_candidates(const RowArgs& a, QLargeLds
       else if (ex + h0 + h1 + h2 >= need) { b = 4 * l + 2; before = ex + h0 + h1; }
       else if (inc >= need) { b = 4 * l + 3; before = ex + h0 + h1 + h2; }
       const uint64_t m = __ballot(b != 0xffffffffu && ex < need);
+      const int w = m ? __builtin_ctzll(m) : 0;
+      const uint32_t bw = rl_u32(b, w), bef = rl_u32(before, w);  // every lane active
       if (l == 0) {
-        const int w = m ? __builtin_ctzll(m) : 0;
-        S.misc[0] = m ? rl_u32(b, w) : 0xffffffffu;
-        S.misc[1] = m ? need - rl_u32(before, w) : 0u;
+        S.misc[0] = m ? bw : 0xffffffffu;
+        S.misc[1] = m ? need - bef : 0u;
       }
     }
     __syncthreads();
@@ -415,6 +502,9 @@ __device__ __forceinline__ void large_finish(const RowArgs& a, QLargeLds& S, int
     return;
   }
   uint32_t flags = row_flags, cut = ns;
+  // without verification outputs the draw's sums themselves are not needed:
+  // the token is taken from a certified approximation where it is clear
+  const bool quick = !a.topk_count && !a.norm;
   if (a.do_topp) {
     // top-p (sampling.rs:255-299) in rank order: e = exp(v - max), S = sequential
     // sum, running sum of e / S, cutoff at the first crossing (kept)
@@ -438,6 +528,30 @@ __device__ __forceinline__ void large_finish(const RowArgs& a, QLargeLds& S, int
     if (cut < ns && (uint32_t)(S.cand[cut - 1] >> 32) == (uint32_t)(S.cand[cut] >> 32)) flags |= TC_FLAG_TIE_CUT;
   }
   const uint64_t last_kept = S.cand[cut - 1];
+  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
+  if (quick) {
+    // the draw: the first kept id whose running sum reaches u (none for u <= 0)
+    uint32_t tok = 0xffffffffu;
+    if (u > 0.0f) {
+      float dq[kLargePer];
+      uint32_t kp = 0;
+#pragma unroll
+      for (int q = 0; q < kLargePer; ++q) {
+        const uint32_t j = kLargePer * t + q;
+        const bool k = j < n_c && S.candv[j] <= last_kept;
+        dq[q] = k ? val_of(S.candv[j]) - vmax : 0.0f;
+        kp |= (k ? 1u : 0u) << q;
+      }
+      const uint32_t f = certified_first<true>(dq, kp, kp, (int)n_c, u, S);
+      if (f != kUndecided) tok = f == 0xffffffffu ? 0u : (uint32_t)S.candv[f];
+    } else {
+      tok = 0u;
+    }
+    if (tok != 0xffffffffu) {
+      finish_row(a, row, tok, TC_OK, flags);
+      return;
+    }
+  }
   // softmax + multinomial in vocabulary order over the kept ids (sampling.rs:302-328)
   float ev[kLargePer], pre2[kLargePer];
   bool kept[kLargePer];
@@ -452,7 +566,6 @@ __device__ __forceinline__ void large_finish(const RowArgs& a, QLargeLds& S, int
 #pragma unroll
   for (int q = 0; q < kLargePer; ++q) pv[q] = kept[q] ? ev[q] / S2 : 0.0f;
   small_seq_prefix(pv, pre2, S);
-  const float u = reinterpret_cast<const float*>(a.uniforms)[row];
   uint32_t first = 0xffffffffu;
   if (u > 0.0f) {
 #pragma unroll
@@ -687,7 +800,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       else if (ex + h0 + h1 + h2 >= K) b = 4 * l + 2;
       else if (inc >= K) b = 4 * l + 3;
       const uint64_t m = __ballot(b != 0xffffffffu && ex < K);
-      if (l == 0) S.misc[0] = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;
+      const uint32_t bw = m ? rl_u32(b, __builtin_ctzll(m)) : 0xffffffffu;  // every lane active
+      if (l == 0) S.misc[0] = bw;
     }
     __syncthreads();
     bK = S.misc[0];

@@ -710,7 +710,7 @@ def test_qwen_large_vocab_keys_far_below_the_max(sampler, kind):
     # the K-th largest key lies more than 256 bf16 keys below the largest:
     # the kernel's full 16-bit radix select
     V = 151936
-    g_ = np.random.default_rng(hash(kind) % 1000)
+    g_ = np.random.default_rng(["spiked", "shifted", "max_subtracted", "peaked"].index(kind) + 17)
     rows = 4
     x = _large_rows(kind, rows, V, g_)
     top = np.argsort(-x, axis=1)[:, :1200]
@@ -721,6 +721,33 @@ def test_qwen_large_vocab_keys_far_below_the_max(sampler, kind):
                dict(temperature=0.9, top_k=64, top_p=1.0, penalty=2.0)):
         print(f"[large] kind={kind} {kw}", flush=True)
         g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, **kw)
+        assert (g["status"] == 0).all(), g["status"]
+        tie = (o["flags"] & 1) != 0
+        same(g, o, rows=[r for r in range(rows) if not tie[r]])
+
+
+@pytest.mark.parametrize("top_k", [50, 1000])
+def test_qwen_large_vocab_kth_key_distances(sampler, top_k):
+    # the K-th largest bf16 key 0, 1, 127, 128, 200, 255 and 256 keys below the
+    # largest (the histogram's first half, its second half, and beyond it),
+    # over a N(0, 1) tail; on half the rows the largest id is in the history
+    V = 151936
+    g_ = np.random.default_rng(top_k)
+    dists = [0, 1, 127, 128, 200, 255, 256, 129]
+    rows = len(dists)
+    x = g_.standard_normal((rows, V)).astype(np.float32)
+    top_bits = 0x4180  # bf16 16.0
+    hist = []
+    for r, dk in enumerate(dists):
+        ids = g_.choice(V, top_k + 20, replace=False)
+        x[r, ids[0]] = np.uint32(top_bits << 16).view(np.float32)
+        x[r, ids[1:top_k]] = np.uint32((top_bits - dk) << 16).view(np.float32)
+        x[r, ids[top_k:]] = np.uint32((top_bits - dk - 3) << 16).view(np.float32)  # just below the K-th
+        hist.append(([int(ids[0])] if r % 2 else []) + g_.integers(0, V, 100).tolist())
+    u = g_.random(rows)
+    for kw in (dict(temperature=0.7, top_p=0.95, penalty=1.1), dict(temperature=1.0, top_p=1.0, penalty=1.0)):
+        print(f"[large] kth distances top_k={top_k} {kw}", flush=True)
+        g, o = run(sampler, O.QWEN, x, hist, u, bf16=True, top_k=top_k, **kw)
         assert (g["status"] == 0).all(), g["status"]
         tie = (o["flags"] & 1) != 0
         same(g, o, rows=[r for r in range(rows) if not tie[r]])

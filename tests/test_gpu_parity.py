@@ -59,7 +59,7 @@ def test_qwen_workloads_bit_exact(sampler, name, batch_index):
         assert np.array_equal(g["keep_probs"][r, :n[r]], o["keep_probs"][r, :n[r]], equal_nan=True), r
 
 
-@pytest.mark.parametrize("name", ["qwen-talker-1x3072", "qwen-cp-512x2048"])
+@pytest.mark.parametrize("name", ["qwen-talker-1x3072", "qwen-cp-512x2048", "qwen-stress-256x151936"])
 @pytest.mark.parametrize("batch_index", [0, 1, 2, 3, 4, 5])
 def test_qwen_workload_ids_without_verification(sampler, name, batch_index):
     # without verification outputs the kernel decides top-p and the draw from
