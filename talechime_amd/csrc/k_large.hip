@@ -38,7 +38,7 @@ static_assert(kLargeCand == 2048 && kLargeThreads == 1024, "block_sort2048 sorts
 
 struct QLargeLds {
   uint4 ltile[kLargeU * kLargeThreads];  // the row's tile kLargeR (chunk kLargeU * t + u at u * blockDim + t)
-  uint32_t bits[kLargeWords];  // history ids and the EOS id
+  uint32_t bits[kLargeWords + 1];  // history ids (k_qwen_large: bit id + shift)
   uint32_t hist[256];
   uint64_t cand[kLargeCand];   // rank order after the sort
   uint64_t candv[kLargeCand];  // vocabulary order
@@ -190,7 +190,7 @@ __device__ __forceinline__ LChunk decode_lchunk(const uint4 v, int q, int shift,
   LChunk c;
   const int e0 = q * 8 - shift;
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  const uint32_t hb = bits_at_fn(bits, nwords, e0);
+  const uint32_t hb = bits_at_fn(bits, nwords, q * 8);  // the bitmap holds id + shift
   c.bad = false;
   c.sn = 0;
 #pragma unroll
@@ -305,13 +305,14 @@ __device__ __forceinline__ uint32_t key16(float v) { return ckey(v) >> 16; }
 // Returns the candidate count (the first kLargeCand staged), or 0xffffffff
 // when a logit is +inf.  NaN logits are left out and the row flagged
 // TC_FLAG_NAN_ROW: the reference's order for them at top-k is unspecified.
-// The history bitmap (S.bits) must be built when the penalty reads it.
+// The history bitmap (S.bits, bit id + boff) must be built when the penalty
+// reads it.
 template <typename InT>
 __device__ __forceinline__ uint32_t large_candidates(const RowArgs& a, QLargeLds& S, int row, int eos,
-                                                     uint32_t* row_flags) {
+                                                     uint32_t* row_flags, int boff) {
   constexpr int E = LargeRow<InT>::kEpc;
   const LargeRow<InT> R(a, row);
-  const int t = threadIdx.x, V = a.V, nwords = (V + 31) >> 5;
+  const int t = threadIdx.x, V = a.V, nwords = (V + boff + 31) >> 5;
   const int tile = kLargeU * (int)blockDim.x;
   const uint32_t K = (uint32_t)a.K;
   const bool use_bits = a.do_pen && a.hist_mode != TC_HIST_MASK;
@@ -328,7 +329,7 @@ __device__ __forceinline__ uint32_t large_candidates(const RowArgs& a, QLargeLds
   // the logits of chunk q (bit h of the result: element h lies in the row)
   auto logits = [&](const uint4& v, int q, float (&lv)[E]) __attribute__((always_inline)) -> uint32_t {
     const int c0 = q * E - R.shift;
-    const uint32_t hb = use_bits ? bits_at_fn(S.bits, nwords, c0) : 0u;
+    const uint32_t hb = use_bits ? bits_at_fn(S.bits, nwords, c0 + boff) : 0u;
     uint32_t in = 0;
 #pragma unroll
     for (int h = 0; h < E; ++h) {
@@ -619,8 +620,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const uint4* base = reinterpret_cast<const uint4*>(rp - shift);
   const int nchunks = (V + shift + 7) >> 3;
   const int eos = (a.eos_id >= 0 && a.eos_id < V) ? a.eos_id : -1;
-  // history bitmap
-  const int nwords = (V + 31) >> 5;
+  // history bitmap, bit id + shift: the bits of chunk q are byte q
+  const int nwords = (V + shift + 31) >> 5;
   for (int w = t; w < nwords; w += blockDim.x) S.bits[w] = 0u;
   if (t < 256) S.hist[t] = 0u;
   __syncthreads();
@@ -629,10 +630,27 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     hist_range(a, row, &h0, &h1);
     for (uint32_t k = h0 + (uint32_t)t; k < h1; k += blockDim.x) {
       const uint32_t id = a.hist_ids[k];
-      if (id < (uint32_t)V) atomicOr(&S.bits[id >> 5], 1u << (id & 31u));
+      const uint32_t b = id + (uint32_t)shift;
+      if (id < (uint32_t)V) atomicOr(&S.bits[b >> 5], 1u << (b & 31u));
     }
   }
   __syncthreads();
+  const uint8_t* hbytes = reinterpret_cast<const uint8_t*>(S.bits);
+  // the chunks holding elements outside the row (q_lo, q_hi) or the EOS id
+  // (-1: none); in_bits and eos_bits give their masks, 0xff and 0 elsewhere
+  const int q_lo = shift ? 0 : -1, q_hi = ((V + shift) & 7) ? nchunks - 1 : -1;
+  const int q_eos = eos >= 0 ? (eos + shift) >> 3 : -1;
+  auto in_bits = [&](int q) __attribute__((always_inline)) -> uint32_t {
+    if (q != q_lo && q != q_hi) return 0xffu;
+    const int c0 = q * 8 - shift;  // in [-7, V)
+    uint32_t inm = 0xffu;
+    if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
+    if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
+    return inm;
+  };
+  auto eos_bits = [&](int q) __attribute__((always_inline)) -> uint32_t {
+    return q == q_eos ? 1u << (uint32_t)(eos + shift - q * 8) : 0u;
+  };
   // the reference's logit after the caller chain and temperature
   // (synthesis.rs:1238-1276, sampling.rs:175-184)
   auto logit = [&](float x, bool sn, int e) { return qlogit(a, x, sn, e, eos); };
@@ -719,12 +737,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
         if (q >= nchunks) break;
-        const int c0 = q * 8 - shift;  // in [-7, V)
-        const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-        uint32_t inm = 0xffu;
-        if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
-        if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
-        const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+        const uint32_t hb = hbytes[q];
+        const uint32_t inm = in_bits(q), em = eos_bits(q);
         const uint32_t live = inm & ~hb & ~em;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -774,12 +788,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
         if (q >= nchunks) break;
-        const int c0 = q * 8 - shift;  // in [-7, V)
-        const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-        uint32_t inm = 0xffu;
-        if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
-        if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
-        const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+        const uint32_t hb = hbytes[q];
+        const uint32_t inm = in_bits(q), em = eos_bits(q);
         const uint32_t live = inm & ~hb & ~em;
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -810,7 +820,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   const float xK = untkey(keyK << 16 | ((keyK & 0x8000u) ? 0u : 0xffffu));
   const float thr = a.do_temp ? xK * a.tmul + 0.0f : xK;  // its logit (not in the history)
   if (bad || bK == 0xffffffffu || (a.do_pen && a.pen_f < 0.0f) || thr == -__builtin_inff()) {
-    n_c = large_candidates<uint16_t>(a, S, row, eos, &row_flags);
+    n_c = large_candidates<uint16_t>(a, S, row, eos, &row_flags, shift);
     if (n_c == 0xffffffffu) {  // a +inf logit: the reference's CDF is NaN -> index 0
       finish_row(a, row, 0u, TC_OK, row_flags);
       no_verify(a, row);
@@ -849,12 +859,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
         if (q < nchunks) {
-          const int c0 = q * 8 - shift;  // in [-7, V)
-          const uint32_t hb = bits_at_fn(S.bits, nwords, c0) & 0xffu;
-          uint32_t inm = 0xffu;
-          if (c0 < 0) inm &= 0xffu << (uint32_t)(-c0);
-          if (c0 + 8 > V) inm &= (1u << (uint32_t)(V - c0)) - 1u;
-          const uint32_t em = (eos >= c0 && eos < c0 + 8) ? 1u << (uint32_t)(eos - c0) : 0u;
+          const uint32_t hb = hbytes[q];
+          const uint32_t inm = in_bits(q), em = eos_bits(q);
           const uint32_t live = inm & ~hb & ~em, pen = inm & hb & ~em;
           uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
   #pragma unroll
@@ -967,7 +973,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large_gen(RowArgs a) {
     return;
   }
   uint32_t row_flags = 0;
-  const uint32_t n_c = large_candidates<InT>(a, S, row, eos, &row_flags);
+  const uint32_t n_c = large_candidates<InT>(a, S, row, eos, &row_flags, 0);
   if (n_c == 0xffffffffu) {  // a +inf logit: the reference's CDF is NaN -> index 0
     finish_row(a, row, 0u, TC_OK, row_flags);
     no_verify(a, row);
