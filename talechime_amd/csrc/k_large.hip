@@ -1,6 +1,8 @@
 // k_large.hip -- qwen sampling over large vocabularies (up to 262,144 logits,
 // one 1024-thread workgroup per row).
 
+#include <type_traits>
+
 #include "tc_row.h"
 
 namespace tc {
@@ -208,6 +210,12 @@ __device__ __forceinline__ LChunk decode_lchunk(const uint4 v, int q, int shift,
 
 __device__ __forceinline__ uint32_t pick_u32(bool c, uint32_t a, uint32_t b) { return c ? a : b; }
 __device__ __forceinline__ uint32_t u4_word(const uint4& v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+__device__ __forceinline__ void u4_set(uint4& v, int i, uint32_t x) {
+  if (i == 0) v.x = x;
+  else if (i == 1) v.y = x;
+  else if (i == 2) v.z = x;
+  else v.w = x;
+}
 
 // ckey(x) >> 16 for the f32 widening of the two bf16 values of a 32-bit word:
 // negative halves complemented, positive ones with the top bit set, -0
@@ -219,6 +227,8 @@ __device__ __forceinline__ uint32_t bkey16x2(uint32_t w) {
   const uint32_t nz = ((w & 0x7fff7fffu) + 0x7fff7fffu) & 0x80008000u;  // low 15 bits nonzero, per half
   return k + ((sgn & ~nz) >> 15);
 }
+// The bf16 bits of a 16-bit key (key 0x8000, shared by both zeros: +0)
+__device__ __forceinline__ uint32_t unkey16(uint32_t k) { return (k & 0x8000u) ? (k & 0x7fffu) : (k ^ 0xffffu); }
 // 0x8000 in each half whose exponent bits are all ones (inf or NaN)
 __device__ __forceinline__ uint32_t nonfinite16x2(uint32_t w) {
   const uint32_t e = (w & 0x7f807f80u) ^ 0x7f807f80u;
@@ -663,13 +673,19 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
   // tile kLargeR is loaded once and kept in LDS, each thread reading back only
   // the slots it wrote; the rest are streamed in every pass, the next tile's
   // loads issued before the current tile's body.  The tile count depends on V
-  // only, so every thread runs every body (pass C's holds barriers).
+  // only, so every thread runs every body (pass C's holds barriers).  Pass A
+  // (fill) turns each word of the register and LDS tiles into its two order
+  // keys (bkey16x2); the body's third argument says whether its chunks hold
+  // keys (std::true_type) or the row's bits.
   const int tile = kLargeU * bd;
   uint4 cache[kLargeR][kLargeU];
   auto tiles = [&](bool fill, auto&& body) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kLargeR; ++i)
-      if (i * tile < nchunks) body(cache[i], i * tile);
+      if (i * tile < nchunks) {
+        if (fill) body(cache[i], i * tile, std::false_type{});
+        else body(cache[i], i * tile, std::true_type{});
+      }
     int tb = kLargeR * tile;
     uint4 raw[kLargeU], nxt[kLargeU];
     if (tb < nchunks) {
@@ -678,10 +694,12 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
       if (fill) {
+        body(raw, tb, std::false_type{});
 #pragma unroll
         for (int u = 0; u < kLargeU; ++u) S.ltile[u * bd + t] = raw[u];
+      } else {
+        body(raw, tb, std::true_type{});
       }
-      body(raw, tb);
       tb += tile;
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
@@ -689,7 +707,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     for (; tb < nchunks; tb += tile) {
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) nxt[u] = base[min(tb + tile + kLargeU * t + u, nchunks - 1)];
-      body(raw, tb);
+      body(raw, tb, std::false_type{});
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) raw[u] = nxt[u];
     }
@@ -732,7 +750,7 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     for (int i = 0; i < kLargeR; ++i)
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) cache[i][u] = base[min(i * tile + kLargeU * t + u, nchunks - 1)];
-    tiles(true, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+    tiles(true, [&](uint4 (&raw)[kLargeU], int tb, auto) __attribute__((always_inline)) {
 #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
@@ -743,9 +761,10 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t w = u4_word(raw[u], j);
-          const uint32_t k2 = bkey16x2(w) & half_mask(live, j);
-          km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(u16x2, k2));
+          const uint32_t kw = bkey16x2(w);
+          km2 = __builtin_elementwise_max(km2, __builtin_bit_cast(u16x2, kw & half_mask(live, j)));
           bad2 |= nonfinite16x2(w) & half_mask(inm, j);
+          u4_set(raw[u], j, kw);
         }
       }
     });
@@ -783,7 +802,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     // (two keys per 32-bit operation; a live key is at most kmax, so its
     // 16-bit distance below kmax does not wrap)
     const u16x2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
-    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb, auto keyed) __attribute__((always_inline)) {
+      constexpr bool kKeyed = decltype(keyed)::value;
   #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
         const int q = tb + kLargeU * t + u;
@@ -793,7 +813,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
         const uint32_t live = inm & ~hb & ~em;
   #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, bkey16x2(u4_word(raw[u], j))));
+          const uint32_t w = u4_word(raw[u], j);
+          const uint32_t d2 = __builtin_bit_cast(uint32_t, kmax2 - __builtin_bit_cast(u16x2, kKeyed ? w : bkey16x2(w)));
           if (((live >> (2 * j)) & 1u) && (d2 & 0xff00u) == 0u) atomicAdd(&S.hist[d2 & 0xffu], 1u);
           if (((live >> (2 * j + 1)) & 1u) && (d2 >> 24) == 0u) atomicAdd(&S.hist[(d2 >> 16) & 0xffu], 1u);
         }
@@ -853,7 +874,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
     // above.
     int parity = 0;
     const uint32_t kK32 = keyK * 0x00010001u, kP32 = keyP * 0x00010001u;  // the thresholds in both halves
-    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb) __attribute__((always_inline)) {
+    tiles(false, [&](const uint4 (&raw)[kLargeU], int tb, auto keyed) __attribute__((always_inline)) {
+      constexpr bool kKeyed = decltype(keyed)::value;
       uint64_t sel = 0, pens = 0;  // bit 8u + h
   #pragma unroll
       for (int u = 0; u < kLargeU; ++u) {
@@ -865,7 +887,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
           uint32_t ge = 0;  // bit h: key >= keyK (live ids) or keyP (the others)
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const uint32_t k2 = bkey16x2(u4_word(raw[u], j));
+            const uint32_t w = u4_word(raw[u], j);
+            const uint32_t k2 = kKeyed ? w : bkey16x2(w);
             const uint32_t th2 = kP32 ^ ((kK32 ^ kP32) & half_mask(live, j));
             const uint32_t m2 = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, k2),
                                                                                        __builtin_bit_cast(u16x2, th2)));
@@ -894,7 +917,8 @@ __global__ void __launch_bounds__(kLargeThreads) k_qwen_large(RowArgs a) {
           for (uint32_t m = (uint32_t)(sel >> (8 * u)) & 0xffu; m; m &= m - 1u) {
             const int h = __builtin_ctz(m);
             const uint32_t wv = pick_u32((h & 4) != 0, pick_u32((h & 2) != 0, w, z), pick_u32((h & 2) != 0, y, x));
-            const uint32_t b = (h & 1) ? (wv & 0xffff0000u) : (wv << 16);
+            const uint32_t hw = (h & 1) ? (wv >> 16) : (wv & 0xffffu);
+            const uint32_t b = (kKeyed ? unkey16(hw) : hw) << 16;
             const int e = (tb + kLargeU * t + u) * 8 - shift + h;
             const float vv = logit(__uint_as_float(b), ((pu >> h) & 1u) != 0u, e);
             const uint64_t kv = ((uint64_t)(~ckey(vv)) << 32) | (uint32_t)e;
