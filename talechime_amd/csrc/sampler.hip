@@ -610,9 +610,12 @@ struct DeviceGuard {
 // Block shape for a register-resident row: ITEMS consecutive elements per
 // thread (a multiple of the 16-byte load width), threads a multiple of 64 in
 // [256, 1024]; rounded up to a multiple of 256 (four waves, one per SIMD) when
-// that still fits, so the SIMDs share the row evenly.
-bool pick_shape(int V, int dtype, int* items, int* threads) {
-  const int pad = dtype == TC_BF16 ? 7 : 3;
+// that still fits, so the SIMDs share the row evenly.  The row may start up
+// to 3 (f32) or 7 (bf16) elements past a 16-byte boundary, unless every row
+// is aligned (`aligned`: the base and the row pitch are multiples of 16
+// bytes).
+bool pick_shape(int V, int dtype, bool aligned, int* items, int* threads) {
+  const int pad = aligned ? 0 : (dtype == TC_BF16 ? 7 : 3);
   static const int f32_items[] = {8, 12, 16, 24}, bf16_items[] = {8, 16, 24};
   const int* its = dtype == TC_BF16 ? bf16_items : f32_items;
   const int n_its = dtype == TC_BF16 ? 3 : 4;
@@ -882,7 +885,9 @@ static int sample_impl(int device, size_t max_vocab, const tc_sample_params* p, 
   }
   if ((size_t)V > max_vocab) return fail(TC_EINVAL, "tc_sample: vocab %d > context max %zu", V, max_vocab);
   int items = 0, threads = 0;
-  if (!pick_shape(V, dtype, &items, &threads) || V > tc::kMaxVocabReg) {
+  const size_t esize = dtype == TC_BF16 ? 2 : 4;
+  const bool aligned = (reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (ld * esize) % 16 == 0;
+  if (!pick_shape(V, dtype, aligned, &items, &threads) || V > tc::kMaxVocabReg) {
     // qwen over bf16 rows up to kLargeVocab: the large-vocabulary kernel
     if (p->variant == TC_QWEN && a.do_pen && (a.pen_f == 0.0f || !isfinite(a.pen_f)))
       return fail(TC_EUNSUPPORTED, "tc_sample: repetition penalty %g above %d logits", p->repetition_penalty,
@@ -1172,7 +1177,9 @@ int tc_greedy_sample(const void* d_logits, int dtype, size_t rows, size_t vocab,
     return fail(TC_EINVAL, "tc_greedy_sample: shape");
   if (dtype != TC_F32 && dtype != TC_BF16) return fail(TC_EINVAL, "tc_greedy_sample: dtype");
   int items, threads;
-  if (!pick_shape((int)vocab, dtype, &items, &threads))
+  const size_t esize = dtype == TC_BF16 ? 2 : 4;
+  const bool aligned = (reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (ld * esize) % 16 == 0;
+  if (!pick_shape((int)vocab, dtype, aligned, &items, &threads))
     return fail(TC_EUNSUPPORTED, "tc_greedy_sample: vocab %zu too large", vocab);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   dim3 g((unsigned)rows), b(threads);
